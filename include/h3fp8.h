@@ -1,0 +1,175 @@
+/*
+ * libh3fp8 -- C ABI of the MI355X (gfx950) online-FP8 linear path of the MiniMax H3 DiT.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, element strides and sizes, and a HIP stream
+ * (`stream` is a `hipStream_t`; NULL = the default stream).  The library never allocates device memory for a call and
+ * never keeps a pointer past the call: the caller (the Python shim, which allocates with torch on the current stream)
+ * owns every input, output and workspace.  Calls are asynchronous on `stream`; the library launches kernels only.
+ *
+ * Status: 0 on success, a negative H3FP8_E* code otherwise, with a message in h3fp8_last_error() (thread-local).
+ *
+ * Layouts (reference: h3_tp2/fp8_gemm.py:362-373, :73; fp8_cutlass.py:93, :111-112):
+ *   a   e4m3fn activations [M, K] row-major, row stride lda (elements = bytes)
+ *   w   e4m3fn weight [N, K] row-major, row stride ldw (the GEMM's B = w^T: torch's `b` with `b.t()` contiguous)
+ *   sa  fp32 per-token scales, element m at sa[m * sa_stride] (sa_stride 0: one scalar scale)
+ *   sb  fp32 per-channel scales, element n at sb[n * sb_stride] (sb_stride 0: one scalar scale)
+ *   y   [M, N] row-major output, row stride ldy, bf16 or fp16 (out_dtype)
+ * Requirements (checked; H3FP8_EINVAL otherwise): K % 16 == 0, N % 16 == 0, 16-byte aligned a/w/y rows
+ * (lda, ldw multiples of 16, ldy multiple of 8), M, N, K >= 0.
+ */
+#ifndef H3FP8_H
+#define H3FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define H3FP8_ABI_VERSION 1
+
+#define H3FP8_OK 0
+#define H3FP8_EINVAL (-22)   /* bad shape, stride, alignment or argument */
+#define H3FP8_EHIP (-5)      /* a HIP runtime call failed */
+
+#define H3FP8_DT_BF16 0
+#define H3FP8_DT_FP16 1
+
+/* ABI version (H3FP8_ABI_VERSION of the build) and the last error of the calling thread. */
+int h3fp8_abi_version(void);
+const char* h3fp8_last_error(void);
+
+/*
+ * One-time set-up of the current device: fills the device-resident SiLU table (65536 bf16 entries) and waits for it.
+ * Every entry point calls it on first use of a device; calling it early keeps that wait out of the hot path.
+ * No counterpart in the reference (its Triton kernels compute exp inline).
+ */
+int h3fp8_init(void);
+
+/*
+ * Kernel 1 -- per-token dynamic FP8 quant of a bf16 [M, K] tensor:
+ *   scale[m] = max(max_k |x[m,k]| / 448, 1/(448*512)),  q[m,k] = e4m3fn_rne(clamp(x[m,k] * (1/scale[m]), +-448)).
+ * Replaces QuantFP8.forward (dynamic, per token) as the reference routes it: h3_tp2/fp8_quant_fuse.py:553-576
+ * (the forward wrapper), :318-327 (launcher `quant`), :280-290 (`_quant_kernel`); same arithmetic as
+ * h3_tp2/ulysses_outq.py:73-93 with one segment.  x rows: stride ldx (elements, multiple of 8); q rows: stride ldq.
+ */
+int h3fp8_quant_rows(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
+                     void* stream);
+
+/*
+ * The same quant when the row maxima are already known (the tail pass of a GEMM whose epilogue reduced them):
+ * scale[m] = max(row_amax[m] / 448, MIN_SCALE), q as above.  x is bf16 [M, K].
+ * Replaces the second half of the fused-quant producers (fp8_quant_fuse.py:105-121, :262-278 after the row max).
+ */
+int h3fp8_quant_rows_amax(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row_amax, void* q,
+                          int64_t ldq, float* scale, void* stream);
+
+/*
+ * Kernel 2 -- scaled FP8 GEMM:  y[m,n] = round(sa[m] * (sb[n] * sum_k a[m,k] w[n,k]))  (fp32 accumulation, K
+ * ascending per lane, no split-K), or round(fma(sa[m], sb[n]*acc, bias[n])) with a bias ([N], in out_dtype).
+ * Replaces ops.cutlass_scaled_mm(a, b=w^T, scale_a, scale_b, out_dtype, bias) as routed by the reference:
+ * h3_tp2/fp8_gemm.py:362-382 (`_mm`), :328-341 (`route`), :149-164 (`scaled_mm_tensor32`), :240-248
+ * (`scaled_mm_fused`); h3_tp2/fp8_cutlass.py:115-131 (`scaled_mm`), fp8_cutlass_kernel.py:698-733 (epilogue).
+ * row_amax: NULL, or an [M] fp32 workspace that receives max_n |y[m,n]| of the rounded outputs (the next layer's
+ * per-token quant fused into this epilogue; finish it with h3fp8_quant_rows_amax).  The library zeroes it first.
+ */
+int h3fp8_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const float* sa, int64_t sa_stride,
+               const float* sb, int64_t sb_stride, const void* bias, void* y, int64_t ldy, int out_dtype, int64_t M,
+               int64_t N, int64_t K, float* row_amax, void* stream);
+
+/*
+ * Kernel 2 + fused next-layer quant: y as h3fp8_gemm (bf16), then q [M, N] e4m3fn + scale [M] of y.
+ * amax_ws: [M] fp32 workspace.  No single counterpart in the reference (its producers fuse the quant instead,
+ * fp8_quant_fuse.py:23-28); the arithmetic is kernel 1's on the bf16 output.
+ */
+int h3fp8_gemm_quant(const void* a, int64_t lda, const void* w, int64_t ldw, const float* sa, int64_t sa_stride,
+                     const float* sb, int64_t sb_stride, const void* bias, void* y, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, float* amax_ws, void* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * Kernel 3 -- gate/up GEMM with the SwiGLU epilogue:  w_gate_up is [2F, K] (gate rows 0..F-1, up rows F..2F-1, vLLM's
+ * merged layout), sb and bias are [2F].  For each (m, f):
+ *   g = bf16(epi(acc[m, f])), u = bf16(epi(acc[m, F+f])), u = (u == 0 ? +0 : u),
+ *   h[m, f] = bf16(bf16(g / (1 + exp(-g))) * u)     (exp correctly rounded; a device table of all 65536 g values)
+ * writes h bf16 [M, F] (row stride ldh) and, if row_amax != NULL, max_f |h[m, f]| into row_amax[m] (zeroed first).
+ * Replaces fp8_swiglu.gemm_swiglu (h3_tp2/fp8_swiglu.py:230-241, kernel :107-157).
+ */
+int h3fp8_gemm_swiglu(const void* a, int64_t lda, const void* w_gate_up, int64_t ldw, const float* sa,
+                      int64_t sa_stride, const float* sb, int64_t sb_stride, const void* bias, void* h, int64_t ldh,
+                      float* row_amax, int64_t M, int64_t F, int64_t K, void* stream);
+
+/*
+ * Kernel 3 with the per-token requant: h3fp8_gemm_swiglu into h_ws (bf16 [M, F], row stride F) with the row maxima in
+ * amax_ws ([M] fp32), then q [M, F] e4m3fn + scale [M] (h3fp8_quant_rows_amax on h_ws).
+ * Replaces fp8_swiglu level 2: scale_swiglu_quant (h3_tp2/fp8_swiglu.py:191-200, kernel :72-103) after the fc1 GEMM.
+ */
+int h3fp8_gemm_swiglu_quant(const void* a, int64_t lda, const void* w_gate_up, int64_t ldw, const float* sa,
+                            int64_t sa_stride, const float* sb, int64_t sb_stride, const void* bias, int64_t M,
+                            int64_t F, int64_t K, void* h_ws, float* amax_ws, void* q, int64_t ldq, float* scale,
+                            void* stream);
+
+/*
+ * Standalone SwiGLU passes (the stash forms of the reference, one wavefront per row):
+ *   h3fp8_scale_swiglu        fp32 product x32 [M, 2F] -> bf16 h [M, F]      (h3_tp2/fp8_swiglu.py:180-188, :47-70)
+ *   h3fp8_scale_swiglu_quant  fp32 product x32 [M, 2F] -> q [M, F] + scale   (h3_tp2/fp8_swiglu.py:191-200, :72-103)
+ *   h3fp8_silu_mul_quant      bf16 [M, 2F] = [gate | up] -> q [M, F] + scale (h3_tp2/fp8_quant_fuse.py:392-402,
+ *                                                                             :262-278)
+ * x32 rows have stride ldx (elements); sa / sb / bias as in h3fp8_gemm (sb, bias [2F]).
+ */
+int h3fp8_scale_swiglu(const float* x32, int64_t ldx, const float* sa, int64_t sa_stride, const float* sb,
+                       int64_t sb_stride, const void* bias, int64_t M, int64_t F, void* h, int64_t ldh, void* stream);
+int h3fp8_scale_swiglu_quant(const float* x32, int64_t ldx, const float* sa, int64_t sa_stride, const float* sb,
+                             int64_t sb_stride, const void* bias, int64_t M, int64_t F, void* q, int64_t ldq,
+                             float* scale, void* stream);
+int h3fp8_silu_mul_quant(const void* x, int64_t ldx, int64_t M, int64_t F, void* q, int64_t ldq, float* scale,
+                         void* stream);
+
+/*
+ * The two-pass scale pass: y = round(sa[m] * (sb[n] * x32[m, n])) (bias: one fma), bf16 or fp16.
+ * Replaces fp8_gemm._scale_bias_cast / _launch (h3_tp2/fp8_gemm.py:37-54, :167-171) and the consumers' stash
+ * materialisation (h3_tp2/fp8_consumers.py:373-380).
+ */
+int h3fp8_scale_bias_cast(const float* x32, int64_t ldx, const float* sa, int64_t sa_stride, const float* sb,
+                          int64_t sb_stride, const void* bias, void* y, int64_t ldy, int out_dtype, int64_t M,
+                          int64_t N, void* stream);
+
+/*
+ * Grouped FP8 GEMM: up to H3FP8_MAX_GROUPS independent h3fp8_gemm problems (bf16 out, no bias) in ONE launch whose
+ * tile space is the concatenation of the groups' tile spaces.  No counterpart in the reference (it launches one GEMM
+ * per linear, fp8_gemm.py:328-341); each group's result equals h3fp8_gemm's on the same operands.
+ */
+#define H3FP8_MAX_GROUPS 8
+typedef struct h3fp8_group {
+    const void* a;
+    int64_t lda;
+    const void* w;
+    int64_t ldw;
+    const float* sa;
+    int64_t sa_stride;
+    const float* sb;
+    int64_t sb_stride;
+    void* y;
+    int64_t ldy;
+    int64_t M, N, K;
+} h3fp8_group;
+
+int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream);
+
+/*
+ * Self-checks used by the install probe and the tests (no reference counterpart beyond its install probes,
+ * h3_tp2/fp8_cutlass.py:196-249):
+ *   h3fp8_selfcheck_e4m3   converts every fp32 bit pattern with |x| <= 448 (and the NaNs) with the hardware cvt used
+ *                          by the kernels and with the software rule of torch's cast; *mismatches (host pointer)
+ *                          receives the count of differing non-NaN results, *nan_bad the NaN inputs not mapped to a
+ *                          NaN code.  Synchronous.
+ *   h3fp8_copy_silu_table  copies the current device's SiLU table (65536 uint16) to `out` (device memory).
+ */
+int h3fp8_selfcheck_e4m3(uint64_t* mismatches, uint64_t* nan_bad);
+int h3fp8_copy_silu_table(void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* H3FP8_H */

@@ -1,0 +1,144 @@
+// Library plumbing of libh3fp8: error reporting, per-device set-up (the SiLU table) and the self-checks.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+
+#include "h3fp8_common.h"
+
+// The bf16 SiLU of every bf16 gate value, one table per device (128 KiB), filled once by h3fp8_init.
+__device__ uint16_t g_h3_silu_table[65536];
+
+// Counters of the e4m3 conversion self-check.
+__device__ unsigned long long g_h3_cvt_counts[2];
+
+namespace {
+thread_local char t_err[512] = "";
+std::mutex g_init_mu;
+constexpr int kMaxDevices = 64;
+bool g_inited[kMaxDevices] = {};
+const uint16_t* g_silu_ptr[kMaxDevices] = {};   // device address of each device's copy of g_h3_silu_table
+}  // namespace
+
+namespace h3host {
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof(t_err), fmt, ap);
+    va_end(ap);
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    set_error("%s failed: %s", what, hipGetErrorString(e));
+    return H3FP8_EHIP;
+}
+
+}  // namespace h3host
+
+// s = bf16(g / (1 + exp(-g))) for every bf16 g (h3_tp2/fp8_swiglu.py:69): exp in float64 rounded once to fp32,
+// then IEEE fp32 add and divide, then RNE to bf16.
+__global__ void __launch_bounds__(256) h3_build_silu_table_kernel() {
+    uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    float g = h3::bf16_to_f32(i);
+    uint32_t r;
+    if (g != g) {
+        r = h3::bf16_rne(g);
+    } else {
+        float e = (float)exp(-(double)g);
+        float d = 1.0f + e;
+        float s = g / d;
+        r = h3::bf16_rne(s);
+    }
+    g_h3_silu_table[i] = (uint16_t)r;
+}
+
+__global__ void __launch_bounds__(256) h3_selfcheck_e4m3_kernel() {
+    unsigned long long bad = 0, nan_bad = 0;
+    const uint64_t total = 1ull << 32;
+    const uint64_t step = (uint64_t)gridDim.x * 256u;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < total; i += step) {
+        float x = h3::u2f((uint32_t)i);
+        bool nan = x != x;
+        if (!nan && !(x >= -H3_FP8_MAX && x <= H3_FP8_MAX)) continue;
+        uint32_t hw = h3::e4m3x2(x, 0.0f) & 0xffu;
+        if (nan) {
+            nan_bad += ((hw & 0x7fu) != 0x7fu);
+        } else {
+            bad += (hw != h3::e4m3_soft(x));
+        }
+    }
+    if (bad) atomicAdd(&g_h3_cvt_counts[0], bad);
+    if (nan_bad) atomicAdd(&g_h3_cvt_counts[1], nan_bad);
+}
+
+__global__ void __launch_bounds__(256) h3_copy_table_kernel(uint16_t* out) {
+    uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    out[i] = g_h3_silu_table[i];
+}
+
+namespace h3host {
+
+int ensure_device_init() {
+    int dev = 0;
+    H3_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("device index %d out of range", dev);
+        return H3FP8_EINVAL;
+    }
+    std::lock_guard<std::mutex> lock(g_init_mu);
+    if (g_inited[dev]) return H3FP8_OK;
+    hipStream_t s;
+    H3_CHECK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    hipLaunchKernelGGL(h3_build_silu_table_kernel, dim3(65536 / 256), dim3(256), 0, s);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipStreamDestroy(s);
+    if (e != hipSuccess) return hip_fail(e, "SiLU table build");
+    void* p = nullptr;
+    H3_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_h3_silu_table)));
+    g_silu_ptr[dev] = (const uint16_t*)p;
+    g_inited[dev] = true;
+    return H3FP8_OK;
+}
+
+const uint16_t* silu_table_ptr() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    return g_silu_ptr[dev];
+}
+
+}  // namespace h3host
+
+extern "C" {
+
+int h3fp8_abi_version(void) { return H3FP8_ABI_VERSION; }
+
+const char* h3fp8_last_error(void) { return t_err; }
+
+int h3fp8_init(void) { return h3host::ensure_device_init(); }
+
+int h3fp8_selfcheck_e4m3(uint64_t* mismatches, uint64_t* nan_bad) {
+    H3_REQUIRE(mismatches && nan_bad, "h3fp8_selfcheck_e4m3: null output pointer");
+    unsigned long long zero[2] = {0, 0};
+    H3_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_h3_cvt_counts), zero, sizeof(zero)));
+    hipLaunchKernelGGL(h3_selfcheck_e4m3_kernel, dim3(4096), dim3(256), 0, (hipStream_t)0);
+    H3_CHECK_HIP(hipGetLastError());
+    H3_CHECK_HIP(hipDeviceSynchronize());
+    unsigned long long out[2];
+    H3_CHECK_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(g_h3_cvt_counts), sizeof(out)));
+    *mismatches = out[0];
+    *nan_bad = out[1];
+    return H3FP8_OK;
+}
+
+int h3fp8_copy_silu_table(void* out, void* stream) {
+    H3_REQUIRE(out, "h3fp8_copy_silu_table: null output");
+    int st = h3host::ensure_device_init();
+    if (st) return st;
+    hipLaunchKernelGGL(h3_copy_table_kernel, dim3(65536 / 256), dim3(256), 0, (hipStream_t)stream, (uint16_t*)out);
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+}  // extern "C"

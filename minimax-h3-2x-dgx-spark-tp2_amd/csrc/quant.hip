@@ -1,0 +1,184 @@
+// Kernel 1: dynamic per-token amax + OCP e4m3fn quant of a bf16 [M, K] tensor (and its "known amax" tail form).
+//
+// Reference arithmetic (h3_tp2/fp8_quant_fuse.py:11-13, :92-121, :280-290, :302-307):
+//   amax = max_k |x_k| (NaN propagating), scale = max(amax / 448, 1/(448*512)),
+//   q_k = e4m3fn_rne(clamp(x_k * (1 / scale), -448, 448)).
+//
+// Design (HBM-bound: 2 bytes read + 1 byte written per element, plus 4 bytes of scale per row):
+//   * one 64-lane wavefront per row; a lane owns CPL chunks of 8 bf16 (16-byte loads), chunk c = lane + 64 j, so every
+//     load instruction of the wave reads 1 KiB of the row contiguously; the row stays in VGPRs (read from HBM once);
+//   * the row maximum is an integer max over |x| bit patterns (for non-negative floats the integer order is the float
+//     order and every NaN pattern is above +inf, so the max propagates NaN exactly like the reference's), reduced
+//     across the wave with xor-shuffles -- no LDS, no barrier;
+//   * scale and 1/scale are IEEE fp32 divisions (hipcc's correctly rounded divide), computed once per lane;
+//   * the e4m3 conversion is gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn, RNE), 8-byte stores per chunk.
+// Four rows per 256-thread workgroup; rows beyond M exit before any memory access.
+#include "h3fp8_common.h"
+
+namespace {
+
+using namespace h3;
+
+// |x| bit patterns of the 8 bf16 values in a 16-byte chunk, max-reduced to one 16-bit pattern.
+__device__ __forceinline__ uint32_t chunk_absmax(uint4 v) {
+    uint32_t m = 0;
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t lo = w[i] & 0x7fffu, hi = (w[i] >> 16) & 0x7fffu;
+        m = m > lo ? m : lo;
+        m = m > hi ? m : hi;
+    }
+    return m;
+}
+
+// 8 bf16 -> 8 e4m3fn bytes with the given inverse scale.
+__device__ __forceinline__ uint2 chunk_quant(uint4 v, float inv) {
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = quant_clamp(u2f(w[i] << 16), inv);
+        f[2 * i + 1] = quant_clamp(u2f(w[i] & 0xffff0000u), inv);
+    }
+    return make_uint2(e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7]));
+}
+
+// One wave per row, CPL 16-byte chunks per lane held in registers.  KNOWN_AMAX: the row maximum comes from row_amax
+// (fp32 bits) instead of the row.
+template <int CPL, bool KNOWN_AMAX>
+__global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
+                                                         int64_t K, uint8_t* __restrict__ q, int64_t ldq,
+                                                         float* __restrict__ scale,
+                                                         const float* __restrict__ row_amax) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int64_t nchunk = K >> 3;
+    const v4u* xr = reinterpret_cast<const v4u*>(x + row * ldx);
+    uint4 v[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        int64_t c = lane + 64 * j;
+        v4u t = (c < nchunk) ? __builtin_nontemporal_load(xr + c) : v4u{0u, 0u, 0u, 0u};
+        v[j] = make_uint4(t.x, t.y, t.z, t.w);
+    }
+    float amax;
+    if (KNOWN_AMAX) {
+        amax = row_amax[row];
+    } else {
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            uint32_t c = chunk_absmax(v[j]);
+            m = m > c ? m : c;
+        }
+        m = wave_max_u32(m);
+        amax = u2f(m << 16);
+    }
+    const float s = row_scale(amax);
+    const float inv = inv_scale(s);
+    uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        int64_t c = lane + 64 * j;
+        if (c < nchunk) qr[c] = chunk_quant(v[j], inv);
+    }
+    if (lane == 0) scale[row] = s;
+}
+
+// Rows too wide for the register-resident form: the row is read twice (max pass, then quant pass).
+template <bool KNOWN_AMAX>
+__global__ void __launch_bounds__(256) quant_rows_wide_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
+                                                              int64_t K, uint8_t* __restrict__ q, int64_t ldq,
+                                                              float* __restrict__ scale,
+                                                              const float* __restrict__ row_amax) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int64_t nchunk = K >> 3;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    float amax;
+    if (KNOWN_AMAX) {
+        amax = row_amax[row];
+    } else {
+        uint32_t m = 0;
+        for (int64_t c = lane; c < nchunk; c += 64) {
+            uint32_t t = chunk_absmax(xr[c]);
+            m = m > t ? m : t;
+        }
+        amax = u2f(wave_max_u32(m) << 16);
+    }
+    const float s = row_scale(amax);
+    const float inv = inv_scale(s);
+    uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
+    for (int64_t c = lane; c < nchunk; c += 64) qr[c] = chunk_quant(xr[c], inv);
+    if (lane == 0) scale[row] = s;
+}
+
+template <bool KNOWN>
+int launch_quant(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
+                 const float* row_amax, hipStream_t st) {
+    if (M == 0) return H3FP8_OK;
+    const int64_t nchunk = K >> 3;
+    const int64_t cpl = (nchunk + 63) / 64;
+    dim3 grid((unsigned)((M + 3) / 4)), block(256);
+    const uint16_t* xp = (const uint16_t*)x;
+    uint8_t* qp = (uint8_t*)q;
+#define H3_Q(N)                                                                                              \
+    hipLaunchKernelGGL((quant_rows_kernel<N, KNOWN>), grid, block, 0, st, xp, ldx, M, K, qp, ldq, scale, row_amax)
+    if (cpl <= 1) H3_Q(1);
+    else if (cpl <= 2) H3_Q(2);
+    else if (cpl <= 3) H3_Q(3);
+    else if (cpl <= 4) H3_Q(4);
+    else if (cpl <= 6) H3_Q(6);
+    else if (cpl <= 8) H3_Q(8);
+    else if (cpl <= 12) H3_Q(12);
+    else if (cpl <= 16) H3_Q(16);
+    else if (cpl <= 24) H3_Q(24);
+    else if (cpl <= 32) H3_Q(32);
+    else hipLaunchKernelGGL((quant_rows_wide_kernel<KNOWN>), grid, block, 0, st, xp, ldx, M, K, qp, ldq, scale, row_amax);
+#undef H3_Q
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+int check_quant_args(const void* x, int64_t ldx, int64_t M, int64_t K, const void* q, int64_t ldq,
+                     const float* scale) {
+    H3_REQUIRE(M >= 0 && K >= 0, "quant: negative size M=%lld K=%lld", (long long)M, (long long)K);
+    H3_REQUIRE(K % 8 == 0, "quant: K=%lld must be a multiple of 8", (long long)K);
+    H3_REQUIRE(M == 0 || (x && q && scale), "quant: null pointer");
+    H3_REQUIRE(ldx >= K && ldx % 8 == 0, "quant: ldx=%lld must be >= K and a multiple of 8", (long long)ldx);
+    H3_REQUIRE(ldq >= K && ldq % 8 == 0, "quant: ldq=%lld must be >= K and a multiple of 8", (long long)ldq);
+    H3_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0, "quant: x must be 16-byte and q 8-byte aligned");
+    return H3FP8_OK;
+}
+
+}  // namespace
+
+namespace h3host {
+// Used by the fused GEMM paths for their tail pass.
+int quant_rows_amax_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row_amax, void* q,
+                           int64_t ldq, float* scale, hipStream_t st) {
+    int rc = check_quant_args(x, ldx, M, K, q, ldq, scale);
+    if (rc) return rc;
+    return launch_quant<true>(x, ldx, M, K, q, ldq, scale, row_amax, st);
+}
+}  // namespace h3host
+
+extern "C" {
+
+int h3fp8_quant_rows(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
+                     void* stream) {
+    int rc = check_quant_args(x, ldx, M, K, q, ldq, scale);
+    if (rc) return rc;
+    return launch_quant<false>(x, ldx, M, K, q, ldq, scale, nullptr, (hipStream_t)stream);
+}
+
+int h3fp8_quant_rows_amax(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row_amax, void* q,
+                          int64_t ldq, float* scale, void* stream) {
+    H3_REQUIRE(M == 0 || row_amax, "quant_rows_amax: null row_amax");
+    return h3host::quant_rows_amax_launch(x, ldx, M, K, row_amax, q, ldq, scale, (hipStream_t)stream);
+}
+
+}  // extern "C"

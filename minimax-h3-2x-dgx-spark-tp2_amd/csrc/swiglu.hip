@@ -1,0 +1,272 @@
+// Standalone SwiGLU / epilogue passes (kernel 3's stash forms) and the two-pass scale pass.
+//
+//   h3fp8_scale_bias_cast     fp32 [M, N] -> bf16/fp16: round(sa * (sb * x)), bias by one fma   (fp8_gemm.py:37-54)
+//   h3fp8_scale_swiglu        fp32 [M, 2F] -> bf16 h [M, F]                                  (fp8_swiglu.py:47-70)
+//   h3fp8_scale_swiglu_quant  fp32 [M, 2F] -> e4m3 q [M, F] + scale [M]                      (fp8_swiglu.py:72-103)
+//   h3fp8_silu_mul_quant      bf16 [M, 2F] -> e4m3 q [M, F] + scale [M]              (fp8_quant_fuse.py:262-278)
+//
+// SwiGLU element (fp8_swiglu.py:64-70): g, u = bf16(epilogue(acc)); u = (u == 0 ? +0 : u);
+// h = bf16(silu_bf16(g) * u), silu_bf16 from the device table of all 65536 bf16 gate values.
+// The row-quant forms run one 256-thread workgroup per row: each thread owns CPT groups of 4 consecutive columns
+// (group c = tid + 256 j), keeps its bf16 h values in registers, and the row maximum is a wave xor-shuffle max plus a
+// 4-entry LDS exchange; the quant then reuses the registers (the row is read from HBM once).
+#include "h3fp8_common.h"
+
+namespace {
+
+using namespace h3;
+
+struct EpiArgs {
+    const float* sa;
+    int64_t sa_stride;
+    const float* sb;
+    int64_t sb_stride;
+    const uint16_t* bias;      // bf16 (or fp16 for scale_bias_cast with fp16 out), may be null
+};
+
+__device__ __forceinline__ float epi(float acc, float sam, float sbn, bool has_bias, float b) {
+    const float t = sbn * acc;
+    return has_bias ? __builtin_fmaf(sam, t, b) : sam * t;
+}
+
+// One SwiGLU element from bf16 gate / up bit patterns.
+__device__ __forceinline__ uint32_t swiglu_bits(uint32_t gb, uint32_t ub, const uint16_t* __restrict__ silu) {
+    float u = bf16_to_f32(ub);
+    u = (u == 0.0f) ? 0.0f : u;
+    return bf16_rne(bf16_to_f32(silu[gb]) * u);
+}
+
+// The 4 h values of column group c (columns 4c .. 4c+3) of row m.
+template <bool SRC_FP32>
+__device__ __forceinline__ void swiglu_group(const void* __restrict__ x, int64_t ldx, int64_t m, int64_t c, int64_t F,
+                                             const EpiArgs& e, float sam, const uint16_t* __restrict__ silu,
+                                             uint32_t h[4]) {
+    const int64_t f = 4 * c;
+    if (SRC_FP32) {
+        const float* xr = reinterpret_cast<const float*>(x) + m * ldx;
+        const v4f ga = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(xr + f));
+        const v4f ua = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(xr + F + f));
+        const float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool hb = e.bias != nullptr;
+            const float bg = hb ? bf16_to_f32(e.bias[f + r]) : 0.f, bu = hb ? bf16_to_f32(e.bias[F + f + r]) : 0.f;
+            const uint32_t gb = bf16_rne(epi(gv[r], sam, e.sb[(f + r) * e.sb_stride], hb, bg));
+            const uint32_t ub = bf16_rne(epi(uv[r], sam, e.sb[(F + f + r) * e.sb_stride], hb, bu));
+            h[r] = swiglu_bits(gb, ub, silu);
+        }
+    } else {
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(x) + m * ldx;
+        const uint2 gw = *reinterpret_cast<const uint2*>(xr + f), uw = *reinterpret_cast<const uint2*>(xr + F + f);
+        h[0] = swiglu_bits(gw.x & 0xffffu, uw.x & 0xffffu, silu);
+        h[1] = swiglu_bits(gw.x >> 16, uw.x >> 16, silu);
+        h[2] = swiglu_bits(gw.y & 0xffffu, uw.y & 0xffffu, silu);
+        h[3] = swiglu_bits(gw.y >> 16, uw.y >> 16, silu);
+    }
+}
+
+__device__ __forceinline__ uint32_t quant4(const uint32_t h[4], float inv) {
+    return e4m3x4(quant_clamp(bf16_to_f32(h[0]), inv), quant_clamp(bf16_to_f32(h[1]), inv),
+                  quant_clamp(bf16_to_f32(h[2]), inv), quant_clamp(bf16_to_f32(h[3]), inv));
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
+    v = wave_max_u32(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    uint32_t r = red[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) r = r > red[i] ? r : red[i];
+    return r;
+}
+
+// One row per workgroup; CPT register-resident column groups per thread (CPT == 0: the row is computed twice).
+template <bool SRC_FP32, int CPT>
+__global__ void __launch_bounds__(256) swiglu_quant_rows_kernel(const void* __restrict__ x, int64_t ldx, int64_t F,
+                                                                EpiArgs e, const uint16_t* __restrict__ silu,
+                                                                uint8_t* __restrict__ q, int64_t ldq,
+                                                                float* __restrict__ scale) {
+    __shared__ uint32_t red[4];
+    const int64_t m = blockIdx.x;
+    const int64_t ngroups = F >> 2;
+    const float sam = SRC_FP32 ? e.sa[m * e.sa_stride] : 1.0f;
+    uint32_t* qr = reinterpret_cast<uint32_t*>(q + m * ldq);
+    uint32_t mx = 0;
+    if (CPT > 0) {
+        uint32_t hv[CPT > 0 ? CPT : 1][4];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int64_t c = threadIdx.x + 256 * j;
+            if (c < ngroups) {
+                swiglu_group<SRC_FP32>(x, ldx, m, c, F, e, sam, silu, hv[j]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t a = (hv[j][r] & 0x7fffu) << 16;
+                    mx = mx > a ? mx : a;
+                }
+            }
+        }
+        const float s = row_scale(u2f(block_max_u32(mx, red)));
+        const float inv = inv_scale(s);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int64_t c = threadIdx.x + 256 * j;
+            if (c < ngroups) qr[c] = quant4(hv[j], inv);
+        }
+        if (threadIdx.x == 0) scale[m] = s;
+    } else {
+        uint32_t hv[4];
+        for (int64_t c = threadIdx.x; c < ngroups; c += 256) {
+            swiglu_group<SRC_FP32>(x, ldx, m, c, F, e, sam, silu, hv);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t a = (hv[r] & 0x7fffu) << 16;
+                mx = mx > a ? mx : a;
+            }
+        }
+        const float s = row_scale(u2f(block_max_u32(mx, red)));
+        const float inv = inv_scale(s);
+        for (int64_t c = threadIdx.x; c < ngroups; c += 256) {
+            swiglu_group<SRC_FP32>(x, ldx, m, c, F, e, sam, silu, hv);
+            qr[c] = quant4(hv, inv);
+        }
+        if (threadIdx.x == 0) scale[m] = s;
+    }
+}
+
+// fp32 product -> bf16 h, elementwise: one thread per group of 4 columns.
+__global__ void __launch_bounds__(256) scale_swiglu_kernel(const float* __restrict__ x, int64_t ldx, int64_t M,
+                                                           int64_t F, EpiArgs e, const uint16_t* __restrict__ silu,
+                                                           uint16_t* __restrict__ h, int64_t ldh) {
+    const int64_t ngroups = F >> 2;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * ngroups) return;
+    const int64_t m = idx / ngroups, c = idx - m * ngroups;
+    uint32_t hv[4];
+    swiglu_group<true>(x, ldx, m, c, F, e, e.sa[m * e.sa_stride], silu, hv);
+    *reinterpret_cast<uint2*>(h + m * ldh + 4 * c) = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
+}
+
+// The two-pass scale pass, elementwise: one thread per 4 columns.
+template <int OUT_DT>
+__global__ void __launch_bounds__(256) scale_bias_cast_kernel(const float* __restrict__ x, int64_t ldx, int64_t M,
+                                                              int64_t N, EpiArgs e, uint16_t* __restrict__ y,
+                                                              int64_t ldy) {
+    const int64_t ngroups = N >> 2;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * ngroups) return;
+    const int64_t m = idx / ngroups, n = 4 * (idx - m * ngroups);
+    const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(x + m * ldx + n));
+    const float xv[4] = {v[0], v[1], v[2], v[3]};
+    const float sam = e.sa[m * e.sa_stride];
+    uint32_t o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const bool hb = e.bias != nullptr;
+        const float b = hb ? (OUT_DT ? fp16_to_f32(e.bias[n + r]) : bf16_to_f32(e.bias[n + r])) : 0.f;
+        const float val = epi(xv[r], sam, e.sb[(n + r) * e.sb_stride], hb, b);
+        o[r] = OUT_DT ? fp16_rne(val) : bf16_rne(val);
+    }
+    *reinterpret_cast<uint2*>(y + m * ldy + n) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+}
+
+template <bool SRC_FP32>
+int launch_swiglu_quant(const void* x, int64_t ldx, int64_t M, int64_t F, const EpiArgs& e, void* q, int64_t ldq,
+                        float* scale, hipStream_t st) {
+    if (M == 0 || F == 0) return H3FP8_OK;
+    int rc = h3host::ensure_device_init();
+    if (rc) return rc;
+    const uint16_t* silu = h3host::silu_table_ptr();
+    const int64_t cpt = ((F >> 2) + 255) / 256;
+    dim3 grid((unsigned)M), block(256);
+    uint8_t* qp = (uint8_t*)q;
+#define H3_S(N) hipLaunchKernelGGL((swiglu_quant_rows_kernel<SRC_FP32, N>), grid, block, 0, st, x, ldx, F, e, silu, \
+                                   qp, ldq, scale)
+    if (cpt <= 1) H3_S(1);
+    else if (cpt <= 2) H3_S(2);
+    else if (cpt <= 4) H3_S(4);
+    else if (cpt <= 8) H3_S(8);
+    else if (cpt <= 16) H3_S(16);
+    else H3_S(0);
+#undef H3_S
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+int check_common(int64_t M, int64_t W, int64_t ldx, const void* x, const char* who) {
+    H3_REQUIRE(M >= 0 && W >= 0, "%s: negative size", who);
+    H3_REQUIRE(W % 8 == 0, "%s: width %lld must be a multiple of 8", who, (long long)W);
+    H3_REQUIRE(M == 0 || x, "%s: null input", who);
+    H3_REQUIRE(ldx >= W && ldx % 4 == 0, "%s: bad row stride %lld", who, (long long)ldx);
+    H3_REQUIRE(((uintptr_t)x & 15) == 0, "%s: input must be 16-byte aligned", who);
+    return H3FP8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int h3fp8_scale_bias_cast(const float* x32, int64_t ldx, const float* sa, int64_t sa_stride, const float* sb,
+                          int64_t sb_stride, const void* bias, void* y, int64_t ldy, int out_dtype, int64_t M,
+                          int64_t N, void* stream) {
+    int rc = check_common(M, N, ldx, x32, "h3fp8_scale_bias_cast");
+    if (rc) return rc;
+    H3_REQUIRE(out_dtype == H3FP8_DT_BF16 || out_dtype == H3FP8_DT_FP16, "h3fp8_scale_bias_cast: bad out_dtype");
+    if (M == 0 || N == 0) return H3FP8_OK;
+    H3_REQUIRE(sa && sb && y && ldy >= N && ldy % 4 == 0 && ((uintptr_t)y & 7) == 0,
+               "h3fp8_scale_bias_cast: bad scales or output");
+    EpiArgs e{sa, sa_stride, sb, sb_stride, (const uint16_t*)bias};
+    const int64_t total = M * (N >> 2);
+    dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    if (out_dtype == H3FP8_DT_BF16)
+        hipLaunchKernelGGL(scale_bias_cast_kernel<0>, grid, block, 0, (hipStream_t)stream, x32, ldx, M, N, e,
+                           (uint16_t*)y, ldy);
+    else
+        hipLaunchKernelGGL(scale_bias_cast_kernel<1>, grid, block, 0, (hipStream_t)stream, x32, ldx, M, N, e,
+                           (uint16_t*)y, ldy);
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+int h3fp8_scale_swiglu(const float* x32, int64_t ldx, const float* sa, int64_t sa_stride, const float* sb,
+                       int64_t sb_stride, const void* bias, int64_t M, int64_t F, void* h, int64_t ldh, void* stream) {
+    int rc = check_common(M, 2 * F, ldx, x32, "h3fp8_scale_swiglu");
+    if (rc) return rc;
+    if (M == 0 || F == 0) return H3FP8_OK;
+    H3_REQUIRE(F % 4 == 0 && sa && sb && h && ldh >= F && ldh % 4 == 0 && ((uintptr_t)h & 7) == 0,
+               "h3fp8_scale_swiglu: bad scales or output");
+    rc = h3host::ensure_device_init();
+    if (rc) return rc;
+    EpiArgs e{sa, sa_stride, sb, sb_stride, (const uint16_t*)bias};
+    const int64_t total = M * (F >> 2);
+    hipLaunchKernelGGL(scale_swiglu_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       x32, ldx, M, F, e, h3host::silu_table_ptr(), (uint16_t*)h, ldh);
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+int h3fp8_scale_swiglu_quant(const float* x32, int64_t ldx, const float* sa, int64_t sa_stride, const float* sb,
+                             int64_t sb_stride, const void* bias, int64_t M, int64_t F, void* q, int64_t ldq,
+                             float* scale, void* stream) {
+    int rc = check_common(M, 2 * F, ldx, x32, "h3fp8_scale_swiglu_quant");
+    if (rc) return rc;
+    if (M == 0 || F == 0) return H3FP8_OK;
+    H3_REQUIRE(F % 4 == 0 && sa && sb && q && scale && ldq >= F && ldq % 4 == 0 && ((uintptr_t)q & 3) == 0,
+               "h3fp8_scale_swiglu_quant: bad scales or output");
+    EpiArgs e{sa, sa_stride, sb, sb_stride, (const uint16_t*)bias};
+    return launch_swiglu_quant<true>(x32, ldx, M, F, e, q, ldq, scale, (hipStream_t)stream);
+}
+
+int h3fp8_silu_mul_quant(const void* x, int64_t ldx, int64_t M, int64_t F, void* q, int64_t ldq, float* scale,
+                         void* stream) {
+    int rc = check_common(M, 2 * F, ldx, x, "h3fp8_silu_mul_quant");
+    if (rc) return rc;
+    if (M == 0 || F == 0) return H3FP8_OK;
+    H3_REQUIRE(F % 4 == 0 && ldx % 8 == 0 && q && scale && ldq >= F && ldq % 4 == 0 && ((uintptr_t)q & 3) == 0,
+               "h3fp8_silu_mul_quant: bad output");
+    EpiArgs e{nullptr, 0, nullptr, 0, nullptr};
+    return launch_swiglu_quant<false>(x, ldx, M, F, e, q, ldq, scale, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,278 @@
+"""Torch-facing launchers of the HIP kernels (allocation with torch on the current stream, raw pointers to the C ABI).
+
+Every function here runs the gfx950 kernels of libh3fp8 on the tensors' device and current stream; there is no CPU or
+PyTorch fallback.  Shapes, dtypes and strides are checked here and again by the C side.
+
+Layouts follow the reference's vLLM call contract (h3_tp2/fp8_gemm.py:362-373): activations ``a`` e4m3fn [M, K]
+row-major; weights as vLLM's ``b`` [K, N] whose transpose ``w = b.t()`` is a row-major [N, K] tensor; per-token scales
+[M, 1] / [M] / scalar; per-channel scales [N] / [1, N] / scalar; bf16 or fp16 output.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+E4M3 = torch.float8_e4m3fn
+FP8_MAX = 448.0
+MIN_SCALE = 1.0 / (FP8_MAX * 512.0)     # vLLM's minimum per-token scale (fp8_quant_fuse.py:78-79)
+
+_DT = {torch.bfloat16: _lib.H3FP8_DT_BF16, torch.float16: _lib.H3FP8_DT_FP16}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need_cuda(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("h3_tp2_amd kernels run on the GPU only; got a CPU tensor")
+
+
+def _rows(t: torch.Tensor, name: str) -> int:
+    """Row stride of a 2-D tensor whose rows are contiguous."""
+    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+        raise ValueError(f"{name} must be 2-D with contiguous rows, got shape {tuple(t.shape)} strides {t.stride()}")
+    return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], t.stride(0))
+
+
+def scale_vec(scale: torch.Tensor, n: int, name: str) -> tuple[torch.Tensor, int]:
+    """(fp32 tensor, element stride) for a per-row/per-column scale of n entries, or a scalar (stride 0)."""
+    if scale.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32, got {scale.dtype}")
+    s = scale.reshape(-1)
+    if s.numel() == 1:
+        return s, 0
+    if s.numel() != n:
+        raise ValueError(f"{name} has {s.numel()} entries, expected {n} or 1")
+    return s, s.stride(0)
+
+
+def init(device=None) -> None:  # noqa: ANN001
+    """One-time set-up of the device (the SiLU table); later calls return at once."""
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        _lib.call("h3fp8_init")
+
+
+# ---- kernel 1 -------------------------------------------------------------------------------------------------------
+
+def quant_rows(x: torch.Tensor, q: torch.Tensor | None = None, scale: torch.Tensor | None = None):
+    """Dynamic per-token quant of a bf16 [M, K] tensor: (q e4m3fn [M, K], scale fp32 [M, 1]).
+    Replaces ``QuantFP8.forward`` / ``fp8_quant_fuse.quant`` (h3_tp2/fp8_quant_fuse.py:318-327)."""
+    _need_cuda(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"quant_rows takes bf16, got {x.dtype}")
+    M, K = x.shape
+    ldx = _rows(x, "x")
+    if q is None:
+        q = torch.empty((M, K), device=x.device, dtype=E4M3)
+    if scale is None:
+        scale = torch.empty((M, 1), device=x.device, dtype=torch.float32)
+    _lib.call("h3fp8_quant_rows", x.data_ptr(), ldx, M, K, q.data_ptr(), _rows(q, "q"), scale.data_ptr(), _stream(x))
+    return q, scale
+
+
+def quant_rows_amax(x: torch.Tensor, row_amax: torch.Tensor, q: torch.Tensor | None = None,
+                    scale: torch.Tensor | None = None):
+    """Per-token quant of bf16 [M, K] with the row maxima given (the tail pass of a fused-amax GEMM)."""
+    _need_cuda(x, row_amax)
+    M, K = x.shape
+    if q is None:
+        q = torch.empty((M, K), device=x.device, dtype=E4M3)
+    if scale is None:
+        scale = torch.empty((M, 1), device=x.device, dtype=torch.float32)
+    _lib.call("h3fp8_quant_rows_amax", x.data_ptr(), _rows(x, "x"), M, K, row_amax.data_ptr(), q.data_ptr(),
+              _rows(q, "q"), scale.data_ptr(), _stream(x))
+    return q, scale
+
+
+# ---- kernel 2 -------------------------------------------------------------------------------------------------------
+
+def _gemm_args(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor, n_cols: int):
+    _need_cuda(a, w, scale_a, scale_b)
+    if a.dtype != E4M3 or w.dtype != E4M3:
+        raise ValueError("a and w must be float8_e4m3fn")
+    if a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)}, w {tuple(w.shape)} (w is [N, K])")
+    M = a.shape[0]
+    sa, sa_st = scale_vec(scale_a, M, "scale_a")
+    sb, sb_st = scale_vec(scale_b, n_cols, "scale_b")
+    return M, sa, sa_st, sb, sb_st
+
+
+def gemm(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+         out_dtype: torch.dtype = torch.bfloat16, bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
+         row_amax: torch.Tensor | None = None) -> torch.Tensor:
+    """y [M, N] = round(sa[m] * (sb[n] * (a @ w.T)[m, n])) (+ bias by one fma); ``w`` is the [N, K] weight.
+    With ``row_amax`` ([M] fp32) the epilogue also reduces max |y| per row (for the next layer's quant)."""
+    N = w.shape[0]
+    M, sa, sa_st, sb, sb_st = _gemm_args(a, w, scale_a, scale_b, N)
+    if out_dtype not in _DT:
+        raise ValueError(f"out_dtype must be bf16 or fp16, got {out_dtype}")
+    if bias is not None and (bias.dim() != 1 or bias.numel() != N or bias.dtype != out_dtype):
+        raise ValueError("bias must be [N] in the output dtype")
+    y = out if out is not None else torch.empty((M, N), device=a.device, dtype=out_dtype)
+    _lib.call("h3fp8_gemm", a.data_ptr(), _rows(a, "a"), w.data_ptr(), _rows(w, "w"), sa.data_ptr(), sa_st,
+              sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, y.data_ptr(), _rows(y, "y"),
+              _DT[out_dtype], M, N, a.shape[1], row_amax.data_ptr() if row_amax is not None else None, _stream(a))
+    return y
+
+
+def scaled_mm(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor, out_dtype: torch.dtype,
+              bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``ops.cutlass_scaled_mm(a, b, scale_a, scale_b, out_dtype, bias)`` with vLLM's ``b`` [K, N] (``b.t()``
+    contiguous): the HIP GEMM (h3_tp2/fp8_gemm.py:149-164 / fp8_cutlass.py:115-131 contract)."""
+    return gemm(a, b.t(), scale_a, scale_b, out_dtype, bias)
+
+
+def gemm_quant(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+               bias: torch.Tensor | None = None):
+    """GEMM to bf16 y plus the per-token e4m3 quant of y fused through the epilogue's row maxima:
+    returns (y bf16 [M, N], q e4m3fn [M, N], scale fp32 [M, 1])."""
+    N = w.shape[0]
+    M, sa, sa_st, sb, sb_st = _gemm_args(a, w, scale_a, scale_b, N)
+    dev = a.device
+    y = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    amax = torch.empty((M,), device=dev, dtype=torch.float32)
+    q = torch.empty((M, N), device=dev, dtype=E4M3)
+    s = torch.empty((M, 1), device=dev, dtype=torch.float32)
+    _lib.call("h3fp8_gemm_quant", a.data_ptr(), _rows(a, "a"), w.data_ptr(), _rows(w, "w"), sa.data_ptr(), sa_st,
+              sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, y.data_ptr(), N, M, N, a.shape[1],
+              amax.data_ptr(), q.data_ptr(), N, s.data_ptr(), _stream(a))
+    return y, q, s
+
+
+# ---- kernel 3 -------------------------------------------------------------------------------------------------------
+
+def gemm_swiglu(a: torch.Tensor, w_gate_up: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                bias: torch.Tensor | None = None, row_amax: torch.Tensor | None = None) -> torch.Tensor:
+    """fc1 + epilogue + SwiGLU in one kernel: bf16 h [M, F] from a [M, K] and the merged [2F, K] gate|up weight
+    (h3_tp2/fp8_swiglu.py:230-241)."""
+    F2 = w_gate_up.shape[0]
+    if F2 % 2:
+        raise ValueError("gate/up weight must have an even number of rows")
+    F = F2 // 2
+    M, sa, sa_st, sb, sb_st = _gemm_args(a, w_gate_up, scale_a, scale_b, F2)
+    h = torch.empty((M, F), device=a.device, dtype=torch.bfloat16)
+    _lib.call("h3fp8_gemm_swiglu", a.data_ptr(), _rows(a, "a"), w_gate_up.data_ptr(), _rows(w_gate_up, "w"),
+              sa.data_ptr(), sa_st, sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, h.data_ptr(),
+              F, row_amax.data_ptr() if row_amax is not None else None, M, F, a.shape[1], _stream(a))
+    return h
+
+
+def gemm_swiglu_quant(a: torch.Tensor, w_gate_up: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                      bias: torch.Tensor | None = None, h_ws: torch.Tensor | None = None):
+    """fc1 + SwiGLU + per-token requant (fp8_swiglu level 2, h3_tp2/fp8_swiglu.py:191-200): (q [M, F], scale [M, 1])."""
+    F2 = w_gate_up.shape[0]
+    F = F2 // 2
+    M, sa, sa_st, sb, sb_st = _gemm_args(a, w_gate_up, scale_a, scale_b, F2)
+    dev = a.device
+    if h_ws is None:
+        h_ws = torch.empty((M, F), device=dev, dtype=torch.bfloat16)
+    amax = torch.empty((M,), device=dev, dtype=torch.float32)
+    q = torch.empty((M, F), device=dev, dtype=E4M3)
+    s = torch.empty((M, 1), device=dev, dtype=torch.float32)
+    _lib.call("h3fp8_gemm_swiglu_quant", a.data_ptr(), _rows(a, "a"), w_gate_up.data_ptr(), _rows(w_gate_up, "w"),
+              sa.data_ptr(), sa_st, sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, M, F,
+              a.shape[1], h_ws.data_ptr(), amax.data_ptr(), q.data_ptr(), F, s.data_ptr(), _stream(a))
+    return q, s
+
+
+def _epi_scales(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, width: int):
+    M = x32.shape[0]
+    s_a, sa_st = scale_vec(sa, M, "sa")
+    s_b, sb_st = scale_vec(sb, width, "sb")
+    return s_a, sa_st, s_b, sb_st
+
+
+def scale_swiglu(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None = None):
+    """fp32 product [M, 2F] -> bf16 SwiGLU [M, F] (h3_tp2/fp8_swiglu.py:180-188)."""
+    _need_cuda(x32, sa, sb)
+    M, W = x32.shape
+    F = W // 2
+    s_a, sa_st, s_b, sb_st = _epi_scales(x32, sa, sb, W)
+    h = torch.empty((M, F), device=x32.device, dtype=torch.bfloat16)
+    _lib.call("h3fp8_scale_swiglu", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), sa_st, s_b.data_ptr(), sb_st,
+              bias.data_ptr() if bias is not None else None, M, F, h.data_ptr(), F, _stream(x32))
+    return h
+
+
+def scale_swiglu_quant(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None = None):
+    """fp32 product [M, 2F] -> SwiGLU -> per-token quant: (q [M, F], scale [M, 1]) (h3_tp2/fp8_swiglu.py:191-200)."""
+    _need_cuda(x32, sa, sb)
+    M, W = x32.shape
+    F = W // 2
+    s_a, sa_st, s_b, sb_st = _epi_scales(x32, sa, sb, W)
+    q = torch.empty((M, F), device=x32.device, dtype=E4M3)
+    s = torch.empty((M, 1), device=x32.device, dtype=torch.float32)
+    _lib.call("h3fp8_scale_swiglu_quant", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), sa_st, s_b.data_ptr(),
+              sb_st, bias.data_ptr() if bias is not None else None, M, F, q.data_ptr(), F, s.data_ptr(),
+              _stream(x32))
+    return q, s
+
+
+def silu_mul_quant(x: torch.Tensor):
+    """silu_and_mul on bf16 [M, 2F] + per-token quant: (q [M, F], scale [M, 1]) (h3_tp2/fp8_quant_fuse.py:392-402)."""
+    _need_cuda(x)
+    M, W = x.shape
+    F = W // 2
+    q = torch.empty((M, F), device=x.device, dtype=E4M3)
+    s = torch.empty((M, 1), device=x.device, dtype=torch.float32)
+    _lib.call("h3fp8_silu_mul_quant", x.data_ptr(), _rows(x, "x"), M, F, q.data_ptr(), F, s.data_ptr(), _stream(x))
+    return q, s
+
+
+def scale_bias_cast(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
+                    out_dtype: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The two-pass scale pass: round(sa * (sb * x32)) (+ bias by one fma) (h3_tp2/fp8_gemm.py:37-54, :167-171)."""
+    _need_cuda(x32, sa, sb)
+    M, N = x32.shape
+    s_a, sa_st, s_b, sb_st = _epi_scales(x32, sa, sb, N)
+    y = out if out is not None else torch.empty((M, N), device=x32.device, dtype=out_dtype)
+    _lib.call("h3fp8_scale_bias_cast", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), sa_st, s_b.data_ptr(),
+              sb_st, bias.data_ptr() if bias is not None else None, y.data_ptr(), _rows(y, "y"), _DT[out_dtype], M, N,
+              _stream(x32))
+    return y
+
+
+# ---- grouped GEMM ---------------------------------------------------------------------------------------------------
+
+def grouped_gemm(problems):  # noqa: ANN001,ANN201
+    """Several (a, w, scale_a, scale_b) problems in one launch; returns their bf16 outputs."""
+    if len(problems) > _lib.MAX_GROUPS:
+        raise ValueError(f"at most {_lib.MAX_GROUPS} groups per launch")
+    arr = (_lib.Group * max(1, len(problems)))()
+    outs, keep = [], []
+    for i, (a, w, scale_a, scale_b) in enumerate(problems):
+        N = w.shape[0]
+        M, sa, sa_st, sb, sb_st = _gemm_args(a, w, scale_a, scale_b, N)
+        y = torch.empty((M, N), device=a.device, dtype=torch.bfloat16)
+        outs.append(y)
+        keep += [sa, sb]
+        arr[i] = _lib.Group(a.data_ptr(), _rows(a, "a"), w.data_ptr(), _rows(w, "w"), sa.data_ptr(), sa_st,
+                            sb.data_ptr(), sb_st, y.data_ptr(), N, M, N, a.shape[1])
+    if problems:
+        _lib.call("h3fp8_grouped_gemm", arr, len(problems), _stream(problems[0][0]))
+    return outs
+
+
+# ---- self-checks ----------------------------------------------------------------------------------------------------
+
+def selfcheck_e4m3() -> tuple[int, int]:
+    """(non-NaN mismatches, NaN inputs not mapped to NaN) of the hardware e4m3 cvt against torch's cast rule, over
+    every fp32 bit pattern in [-448, 448] and every NaN (synchronous)."""
+    bad, nan_bad = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    _lib.call("h3fp8_selfcheck_e4m3", ctypes.byref(bad), ctypes.byref(nan_bad))
+    return int(bad.value), int(nan_bad.value)
+
+
+def silu_table(device=None) -> torch.Tensor:  # noqa: ANN001
+    """The device's SiLU table (65536 bf16 bit patterns as int16)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    out = torch.empty(65536, device=dev, dtype=torch.int16)
+    with torch.cuda.device(dev):
+        _lib.call("h3fp8_copy_silu_table", out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+    return out

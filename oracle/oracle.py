@@ -1,0 +1,230 @@
+"""CPU oracle of the online-FP8 linear path -- TEST INFRASTRUCTURE ONLY.
+
+Python face of ``oracle.c`` (built by ``make -C oracle`` into ``liboracle.so``) plus the fp32 matmul in numpy.  Only
+``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import this module, and only to
+check or to time the reference algorithm; the product path never calls it.
+
+Each function names the reference code it restates (paths relative to the reference checkout):
+
+* ``quant_rows``          h3_tp2/fp8_quant_fuse.py:302-307 (``quant_torch``), formula at :11-13, helpers :92-121
+* ``e4m3fn_from_f32``     the ``.to(torch.float8_e4m3fn)`` cast of fp8_quant_fuse.py:306
+* ``bf16_rne``            h3_tp2/fp8_swiglu.py:38-45 (``_round_bf16``) and torch's fp32 -> bf16 cast
+* ``epilogue``            h3_tp2/fp8_gemm.py:37-54, :120-126, :174-185 (``sb * acc`` first, then ``sa``; bias by fma)
+* ``silu_table``          h3_tp2/fp8_swiglu.py:69, :211 (``bf16(g / (1 + exp(-g)))``, exp correctly rounded here)
+* ``swiglu_bf16``         h3_tp2/fp8_swiglu.py:64-70, :210-212; fp8_quant_fuse.py:262-278 (before its quant)
+* ``scale_swiglu``        h3_tp2/fp8_swiglu.py:47-70, :203-212
+* ``scale_swiglu_quant``  h3_tp2/fp8_swiglu.py:72-103
+* ``dequant_matmul``      h3_tp2/fp8_consumers.py:518-523 (``a.float() @ w.float().t()``, fp32); ``matmul_f32`` is the
+                          same product through numpy's BLAS (any summation order) for large shapes.
+
+Pinning (what each function is checked against, in tests/test_oracle.py): the e4m3fn/bf16/fp16 casts against torch's
+and numpy's own casts on exhaustive or dense sweeps; ``quant_rows`` against known answers of the reference's tests
+(zero row -> MIN_SCALE, every positive finite bf16 as a row maximum against IEEE division done by numpy), against the
+e4m3 grid (every code re-quantises to itself) and against brute-force nearest-grid search; ``epilogue`` against the
+order-sensitive known answer of tests/test_fp8_gemm.py:67-75 and against float64 arithmetic; ``silu_table`` against
+torch's CPU exp on all 65536 bf16 inputs and against float64; ``dequant_matmul`` against exact integer products.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+FP8_MAX = 448.0
+MIN_SCALE = np.float32(1.0 / (448.0 * 512.0))
+
+
+def build(force: bool = False) -> str:
+    """Compile ``oracle.c`` with the committed Makefile (gcc); returns the library path."""
+    src = os.path.join(_HERE, "oracle.c")
+    if force or not os.path.exists(_LIB_PATH) or os.path.getmtime(_LIB_PATH) < os.path.getmtime(src):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.oracle_quant_rows.argtypes = [P, I64, I64, I64, P, I64, P]
+        L.oracle_epilogue.argtypes = [P, I64, I64, P, P, P, I, P]
+        L.oracle_silu_table.argtypes = [P]
+        L.oracle_swiglu_bf16.argtypes = [P, I64, I64, I64, P]
+        L.oracle_scale_swiglu.argtypes = [P, I64, I64, P, P, P, P]
+        L.oracle_scale_swiglu_quant.argtypes = [P, I64, I64, P, P, P, P, P]
+        L.oracle_dequant_matmul.argtypes = [P, I64, P, I64, I64, I64, I64, P]
+        L.oracle_e4m3fn_from_f32.argtypes = [ctypes.c_float]
+        L.oracle_e4m3fn_from_f32.restype = ctypes.c_uint8
+        L.oracle_bf16_rne.argtypes = [ctypes.c_float]
+        L.oracle_bf16_rne.restype = ctypes.c_uint16
+        L.oracle_min_scale.restype = ctypes.c_float
+        for name in ("oracle_e4m3fn_from_f32_array", "oracle_bf16_rne_array", "oracle_fp16_rne_array"):
+            getattr(L, name).argtypes = [P, I64, P]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _u16(a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint16) if a.dtype.itemsize == 2 else a.astype(np.uint16)
+
+
+def bf16_bits_from_f32(x: np.ndarray) -> np.ndarray:
+    """Vectorised fp32 -> bf16 RNE bits (same rule as oracle_bf16_rne, NaN quietened)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
+    """Decode e4m3fn codes (uint8) to fp32 through a 256-entry table."""
+    return _E4M3_LUT()[np.asarray(codes, dtype=np.uint8)]
+
+
+_lut_cache: dict = {}
+
+
+def _E4M3_LUT() -> np.ndarray:
+    t = _lut_cache.get("e4m3")
+    if t is None:
+        f = lib().oracle_e4m3fn_to_f32
+        f.argtypes = [ctypes.c_uint8]
+        f.restype = ctypes.c_float
+        t = np.array([f(i) for i in range(256)], dtype=np.float32)
+        _lut_cache["e4m3"] = t
+    return t
+
+
+def e4m3fn_from_f32(x: np.ndarray) -> np.ndarray:
+    """Elementwise fp32 -> e4m3fn (RNE) through the C routine (the ``.to(float8_e4m3fn)`` of the reference)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(x.size, dtype=np.uint8)
+    lib().oracle_e4m3fn_from_f32_array(_p(x), x.size, _p(out))
+    return out
+
+
+def bf16_rne(x: np.ndarray) -> np.ndarray:
+    """Elementwise fp32 -> bf16 bits through the C routine (``_round_bf16`` / torch's cast)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().oracle_bf16_rne_array(_p(x), x.size, _p(out))
+    return out
+
+
+def fp16_rne(x: np.ndarray) -> np.ndarray:
+    """Elementwise fp32 -> fp16 bits through the C routine (torch's ``.to(torch.float16)``)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().oracle_fp16_rne_array(_p(x), x.size, _p(out))
+    return out
+
+
+def quant_rows(x_bf16_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """bf16 [M, K] (uint16 bit patterns) -> (e4m3fn codes uint8 [M, K], fp32 scale [M])."""
+    x = _u16(x_bf16_bits)
+    M, K = x.shape
+    q = np.empty((M, K), dtype=np.uint8)
+    s = np.empty((M,), dtype=np.float32)
+    lib().oracle_quant_rows(_p(x), M, K, K, _p(q), K, _p(s))
+    return q, s
+
+
+def epilogue(acc: np.ndarray, sa: np.ndarray, sb: np.ndarray, bias_bits: np.ndarray | None = None,
+             out_fp16: bool = False) -> np.ndarray:
+    """fp32 [M, N] accumulator -> bf16 (or fp16) bit patterns [M, N]: round(sa[m] * (sb[n] * acc)), bias by fma."""
+    acc = np.ascontiguousarray(acc, dtype=np.float32)
+    M, N = acc.shape
+    sa = np.ascontiguousarray(np.broadcast_to(np.asarray(sa, np.float32).reshape(-1), (M,)))
+    sb = np.ascontiguousarray(np.broadcast_to(np.asarray(sb, np.float32).reshape(-1), (N,)))
+    b = None if bias_bits is None else _u16(bias_bits)
+    y = np.empty((M, N), dtype=np.uint16)
+    lib().oracle_epilogue(_p(acc), M, N, _p(sa), _p(sb), None if b is None else _p(b), int(out_fp16), _p(y))
+    return y
+
+
+def silu_table() -> np.ndarray:
+    """bf16 bits g -> bf16 bits of silu(g) rounded to bf16, for all 65536 inputs."""
+    t = _lut_cache.get("silu")
+    if t is None:
+        t = np.empty(65536, dtype=np.uint16)
+        lib().oracle_silu_table(_p(t))
+        _lut_cache["silu"] = t
+    return t
+
+
+def swiglu_bf16(gu_bits: np.ndarray) -> np.ndarray:
+    """bf16 [M, 2F] = [gate | up] -> bf16 h [M, F] (bit patterns)."""
+    gu = _u16(gu_bits)
+    M, W = gu.shape
+    F = W // 2
+    h = np.empty((M, F), dtype=np.uint16)
+    lib().oracle_swiglu_bf16(_p(gu), M, F, W, _p(h))
+    return h
+
+
+def scale_swiglu(acc: np.ndarray, sa: np.ndarray, sb: np.ndarray, bias_bits: np.ndarray | None = None) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, dtype=np.float32)
+    M, W = acc.shape
+    F = W // 2
+    sa = np.ascontiguousarray(sa, dtype=np.float32).reshape(-1)
+    sb = np.ascontiguousarray(sb, dtype=np.float32).reshape(-1)
+    b = None if bias_bits is None else _u16(bias_bits)
+    h = np.empty((M, F), dtype=np.uint16)
+    lib().oracle_scale_swiglu(_p(acc), M, F, _p(sa), _p(sb), None if b is None else _p(b), _p(h))
+    return h
+
+
+def scale_swiglu_quant(acc: np.ndarray, sa: np.ndarray, sb: np.ndarray, bias_bits: np.ndarray | None = None):
+    acc = np.ascontiguousarray(acc, dtype=np.float32)
+    M, W = acc.shape
+    F = W // 2
+    sa = np.ascontiguousarray(sa, dtype=np.float32).reshape(-1)
+    sb = np.ascontiguousarray(sb, dtype=np.float32).reshape(-1)
+    b = None if bias_bits is None else _u16(bias_bits)
+    q = np.empty((M, F), dtype=np.uint8)
+    s = np.empty((M,), dtype=np.float32)
+    lib().oracle_scale_swiglu_quant(_p(acc), M, F, _p(sa), _p(sb), None if b is None else _p(b), _p(q), _p(s))
+    return q, s
+
+
+def dequant_matmul(a_codes: np.ndarray, w_codes: np.ndarray) -> np.ndarray:
+    """fp32 acc[m, n] = sum_k a[m, k] * w[n, k] (K ascending, C loop; small shapes)."""
+    a = np.ascontiguousarray(a_codes, dtype=np.uint8)
+    w = np.ascontiguousarray(w_codes, dtype=np.uint8)
+    M, K = a.shape
+    N = w.shape[0]
+    acc = np.empty((M, N), dtype=np.float32)
+    lib().oracle_dequant_matmul(_p(a), K, _p(w), K, M, N, K, _p(acc))
+    return acc
+
+
+def matmul_f32(a_codes: np.ndarray, w_codes: np.ndarray) -> np.ndarray:
+    """The same fp32 product through numpy's BLAS (multithreaded, any summation order): large shapes."""
+    lut = _E4M3_LUT()
+    return lut[a_codes] @ lut[w_codes].T
+
+
+def linear(x_bf16_bits: np.ndarray, w_codes: np.ndarray, sb: np.ndarray, bias_bits=None, out_fp16=False):
+    """The whole reference CPU path of one online-FP8 linear: per-token quant of X, fp32 product, epilogue."""
+    q, sa = quant_rows(x_bf16_bits)
+    return epilogue(matmul_f32(q, w_codes), sa, sb, bias_bits, out_fp16), q, sa

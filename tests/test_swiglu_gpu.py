@@ -1,0 +1,111 @@
+"""Kernel 3 (SwiGLU epilogue + per-token requant) and its standalone forms against the oracle, bit for bit.
+
+Follows the reference's tests/test_fp8_swiglu.py:17-45, :91-105 (random and directed gate values: +-0, subnormals,
++-88, +-1e4, midpoints, +-inf, NaN, a masked tail) and tests/test_fp8_quant_fuse_gpu.py:93-103 (silu_and_mul + quant
+with directed gate/up pairs).  The fused GEMM + SwiGLU is exact on integer-valued operands (exact accumulators).
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_quant_equal, bits16, bits8, f32, int_operands, serving_like
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _nan_aware_equal(out_bits: np.ndarray, ref_bits: np.ndarray):
+    nan_ref = (ref_bits & 0x7FFF) > 0x7F80
+    nan_out = (out_bits & 0x7FFF) > 0x7F80
+    assert np.array_equal(nan_out, nan_ref), "NaN positions differ"
+    bad = (out_bits != ref_bits) & ~nan_ref
+    assert not bad.any(), f"{int(bad.sum())} bf16 values differ, first at {np.argwhere(bad)[:5].tolist()}"
+
+
+def test_silu_table_exhaustive(cuda):
+    from h3_tp2_amd import ops
+    tab = ops.silu_table(cuda).cpu().numpy().view(np.uint16)
+    _nan_aware_equal(tab, O.silu_table())
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("M,width", [(64, 256), (300, 28672), (33, 16384)])
+def test_scale_swiglu_random(cuda, M, width, bias):
+    from h3_tp2_amd import ops
+    g = torch.Generator().manual_seed(M + width)
+    x32 = torch.randn(M, width, generator=g) * 3000          # gate values up to ~ +-15 after the scales
+    sa = torch.rand(M, generator=g) * 0.01 + 0.001
+    sb = torch.rand(width, generator=g) * 0.01 + 0.001
+    bb = (torch.randn(width, generator=g) * 0.1).to(torch.bfloat16) if bias else None
+    h = ops.scale_swiglu(x32.to(cuda), sa.to(cuda), sb.to(cuda), bb.to(cuda) if bias else None)
+    q, s = ops.scale_swiglu_quant(x32.to(cuda), sa.to(cuda), sb.to(cuda), bb.to(cuda) if bias else None)
+    torch.cuda.synchronize()
+    bbits = bits16(bb) if bias else None
+    _nan_aware_equal(bits16(h), O.scale_swiglu(x32.numpy(), sa.numpy(), sb.numpy(), bbits))
+    assert_quant_equal(q, s, *O.scale_swiglu_quant(x32.numpy(), sa.numpy(), sb.numpy(), bbits))
+
+
+def test_scale_swiglu_directed_values(cuda):
+    from h3_tp2_amd import ops
+    width = 2 * 1500
+    vals = torch.tensor([0.0, -0.0, 1e-40, -1e-40, 1.0, -1.0, 88.0, -88.0, 1e4, -1e4, 0.5000001, 1.9999999,
+                         float("inf"), -float("inf"), float("nan")])
+    x32 = vals.repeat(1, width // vals.numel() + 1)[:, :width].clone()
+    x32 = torch.cat([x32, torch.randn(7, width, generator=torch.Generator().manual_seed(9)) * 100])
+    sa = torch.ones(x32.shape[0])
+    sb = torch.ones(width)
+    h = ops.scale_swiglu(x32.to(cuda), sa.to(cuda), sb.to(cuda))
+    torch.cuda.synchronize()
+    _nan_aware_equal(bits16(h), O.scale_swiglu(x32.numpy(), sa.numpy(), sb.numpy()))
+
+
+@pytest.mark.parametrize("M,F", [(1, 14336), (200, 14336), (64, 8192), (5, 40000)])
+def test_silu_mul_quant(cuda, M, F):
+    from h3_tp2_amd import ops
+    g = torch.Generator().manual_seed(M + 3)
+    h = (torch.randn(M, 2 * F, generator=g) * 4).to(torch.bfloat16)
+    h[:, :7] = torch.tensor([0.0, -0.0, 1e-38, -88.0, 88.0, 3.0, -3.0]).to(torch.bfloat16)
+    h[:, F:F + 7] = torch.tensor([-0.0, 0.0, -0.0, 1.0, -1.0, -0.0, 0.0]).to(torch.bfloat16)
+    q, s = ops.silu_mul_quant(h.to(cuda))
+    torch.cuda.synchronize()
+    hh = O.swiglu_bf16(bits16(h))
+    assert_quant_equal(q, s, *O.quant_rows(hh))
+
+
+@pytest.mark.parametrize("M,F,K", [(200, 320, 512), (333, 1024, 1024), (257, 4096, 3072), (64, 8192, 256),
+                                   (1, 128, 64)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_gemm_swiglu_integer_exact(cuda, M, F, K, bias):
+    from h3_tp2_amd import ops
+    a, w, sa, sb = int_operands(M, 2 * F, K, seed=M + F + K, device=cuda)
+    # scales chosen so the gate values span the interesting part of silu (|g| up to ~10)
+    sb = sb * 40.0
+    bb = (torch.randn(2 * F, generator=torch.Generator().manual_seed(1)) * 0.5).to(torch.bfloat16).to(cuda) \
+        if bias else None
+    acc = O.matmul_f32(bits8(a), bits8(w))
+    bbits = bits16(bb) if bias else None
+    h_ref = O.scale_swiglu(acc, f32(sa), f32(sb), bbits)
+    amax = torch.full((M,), 5.0, device=cuda)
+    h = ops.gemm_swiglu(a, w, sa, sb, bb, row_amax=amax)
+    q, s = ops.gemm_swiglu_quant(a, w, sa, sb, bb)
+    torch.cuda.synchronize()
+    _nan_aware_equal(bits16(h), h_ref)
+    assert torch.equal(amax, h.float().abs().amax(dim=1))
+    assert_quant_equal(q, s, *O.scale_swiglu_quant(acc, f32(sa), f32(sb), bbits))
+
+
+@pytest.mark.parametrize("M", [200, 1000])
+def test_gemm_swiglu_random_within_tolerance(cuda, M):
+    """Serving-like fc1 operands: the fused kernel vs the oracle's SwiGLU of the fp32 product; the SwiGLU output is
+    within 2e-2 * rms and >= 95 % bit-equal (accumulation order only)."""
+    from h3_tp2_amd import ops
+    F, K = 4096, 5376
+    a, w, sa, sb = serving_like(M, 2 * F, K, seed=M + 17, device=cuda)
+    h = ops.gemm_swiglu(a, w, sa, sb)
+    torch.cuda.synchronize()
+    h_ref = O.scale_swiglu(O.matmul_f32(bits8(a), bits8(w)), f32(sa), f32(sb))
+    ref = torch.from_numpy(h_ref.view(np.int16)).view(torch.bfloat16).float().numpy()
+    out = f32(h)
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    assert float(np.max(np.abs(out - ref))) <= 2e-2 * rms
+    assert float(np.mean(bits16(h) == h_ref)) >= 0.95
