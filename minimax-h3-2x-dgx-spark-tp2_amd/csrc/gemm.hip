@@ -6,16 +6,23 @@
 //   accumulator, no split-K; with a bias: round(fma(sa[m], sb[n] * acc, bias[n])).
 //
 // Tiling (one workgroup = 4 wavefronts = 256 threads, one workgroup per CU):
-//   * block tile 256 (tokens m) x 256 (channels n) x 128 (k); each wave owns a 128 x 128 sub-tile: 8 x 8 MFMA tiles of
-//     v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3 -> fp32), 256 fp32 accumulators per lane;
-//   * the MFMA's A operand is the weight tile (rows n) and its B operand the activation tile (rows m), so a lane's four
-//     accumulators of an MFMA tile are four consecutive channels n of one token m: the epilogue stores 8 bytes per lane;
-//   * global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging): each instruction moves 8 rows x 128 bytes;
+//   * block tile 256 (tokens m) x 256 (channels n) x 128 (k); each wave owns a 128 x 128 sub-tile: 4 x 4 MFMA tiles of
+//     v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3 -> fp32), two k sub-steps per stage, 256 fp32 accumulators per lane (the
+//     AGPR file);
+//   * the MFMA's A operand is the weight tile (rows n) and its B operand the activation tile (rows m), so each group of
+//     four accumulators of a lane holds four consecutive channels n of one token m: the epilogue stores 8 bytes;
+//   * global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging): each instruction moves 8 rows x 128 bytes, i.e.
+//     whole 128-byte lines (64-byte row pieces halve the load path's throughput: measured 22 vs 40 bytes/clk/CU);
 //     out-of-range rows and the K tail read as zero through the buffer descriptor's range check;
-//   * LDS rows are 128 bytes (one k-step); 16-byte chunk c of row r is stored at chunk c ^ (r & 7), so the eight lanes
-//     of an MFMA operand read that share a chunk index hit eight different bank groups;
-//   * two LDS stages (2 x 64 KiB): the loads of k-step i+1 are in flight while k-step i is multiplied; one barrier
-//     per k-step, after every wave's ds_reads of the stage have completed (lgkmcnt(0)) -- the stage-release rule;
+//   * two LDS stages (2 x 64 KiB); a stage is released by a barrier right after the last reads of its k-step (early in
+//     the step), so the loads of k-step i+2 run during about 44 MFMAs (about 1.5 k-steps);
+//   * LDS rows are 128 bytes; 16-byte chunk c of row r is stored at chunk c ^ swz(r), swz(r) = ((r >> 1) & 7) ^
+//     ((r & 1) << 2): eight consecutive rows (32 banks) and sixteen (64 banks) read at one logical chunk never share a
+//     bank (conflict-free ds_read_b128);
+//   * operand fragments are double-buffered in VGPRs: sub-step 1 is read while sub-step 0 multiplies, and the next
+//     stage's sub-step 0 right after the barrier that publishes it, while the last MFMAs of the step run;
+//   * stage release: a stage is refilled only after a barrier that every wave reaches with lgkmcnt(0), i.e. after all
+//     of its ds_reads have returned;
 //   * tile order: workgroups are spread over the 8 XCDs round-robin by the hardware, so the block index is remapped to
 //     give every XCD a contiguous range of tiles, walked in groups of GROUP_M row tiles (L2 reuse of both operands).
 // SwiGLU variant: the weight tile is 128 gate rows f0.. and the 128 matching up rows F+f0..; each wave holds the gate
@@ -28,12 +35,16 @@ namespace {
 
 using namespace h3;
 
+typedef float v16f __attribute__((ext_vector_type(16)));
+
 constexpr int BM = 256;          // tokens per block tile
 constexpr int BN = 256;          // weight rows per block tile
-constexpr int BK = 128;          // k per step = one MFMA's K
-constexpr int STAGE_BYTES = (BM + BN) * BK;   // 64 KiB
+constexpr int BK = 128;          // k per stage: 128-byte row pieces
+constexpr int ROWB = BK;         // bytes per LDS row
+constexpr int STAGE_BYTES = (BM + BN) * ROWB;   // 64 KiB
 constexpr int NSTAGE = 2;
-constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;
+constexpr int A_REGION = BN * ROWB;             // activation rows start after the weight rows
+constexpr int MFMA_SPLIT = 12;                  // sub-step-1 MFMAs issued before the stage barrier (of 16)
 constexpr uint32_t OOB = 0x80000000u;         // an offset past every buffer's range: the load returns zeros
 
 enum Epi { EPI_PLAIN = 0, EPI_AMAX = 1, EPI_SWIGLU = 2 };
@@ -56,9 +67,6 @@ struct GemmParams {
     int tile_offset;           // grouped launches: first block of this problem
 };
 
-__device__ __forceinline__ void waitcnt_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }     // vmcnt(0)
-__device__ __forceinline__ void waitcnt_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }   // lgkmcnt(0)
-
 // block index -> (tile_m, tile_n): XCD-contiguous ranges, then GROUP_M-row groups (column-major inside a group).
 __device__ __forceinline__ void tile_of(int b, int T, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
     const int xcd = b & 7, local = b >> 3;
@@ -73,11 +81,18 @@ __device__ __forceinline__ void tile_of(int b, int T, int tiles_m, int tiles_n, 
     tn = r / gsz;
 }
 
-__device__ __forceinline__ v8i read_frag(const uint8_t* region, int row, int g) {
-    const uint8_t* p = region + row * BK;
-    const int s = row & 7;
-    uint4 lo = *reinterpret_cast<const uint4*>(p + (((2 * g) ^ s) << 4));
-    uint4 hi = *reinterpret_cast<const uint4*>(p + (((2 * g + 1) ^ s) << 4));
+// LDS chunk swizzle (see the header): logical 16-byte chunk c of row r is stored at chunk c ^ swz(r).
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+
+// One 32 x 64 MFMA operand of k sub-step `sub`: lane l reads row (l & 31) of the tile, logical chunks 4 sub + 2h and
+// 4 sub + 2h + 1 (h = l >> 5).  Tile bases are multiples of 32 rows, so swz of the tile row equals swz of the LDS row.
+__device__ __forceinline__ v8i read_frag(const uint8_t* tile, int lane, int sub) {
+    const int row = lane & 31, h = lane >> 5;
+    const uint8_t* p = tile + row * ROWB;
+    const int s = swz(row);
+    const int c0 = 4 * sub + 2 * h;
+    const uint4 lo = *reinterpret_cast<const uint4*>(p + ((c0 ^ s) << 4));
+    const uint4 hi = *reinterpret_cast<const uint4*>(p + (((c0 + 1) ^ s) << 4));
     v8i f;
     f[0] = (int)lo.x; f[1] = (int)lo.y; f[2] = (int)lo.z; f[3] = (int)lo.w;
     f[4] = (int)hi.x; f[5] = (int)hi.y; f[6] = (int)hi.z; f[7] = (int)hi.w;
@@ -89,8 +104,185 @@ __device__ __forceinline__ float load_bias(const void* bias, int n, int out_dt) 
     return out_dt ? fp16_to_f32(b) : bf16_to_f32(b);
 }
 
+// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt
+// and lgkmcnt left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); }
+
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// Workgroup barrier without a memory-model fence: __syncthreads() would add a release fence that waits for every
+// in-flight LDS-DMA load (vmcnt(0)), including the k-steps still being prefetched.  The explicit vmcnt/lgkmcnt waits
+// before it carry the ordering; the "memory" clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
+
+// A buffer descriptor as four dwords (base, stride 0, num_records = byte range, gfx9 raw-buffer flags); loads at
+// offsets >= num_records return zeros.
+__device__ __forceinline__ v4u buffer_desc(const void* base, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    v4u d;
+    d[0] = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    d[1] = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu);
+    d[2] = __builtin_amdgcn_readfirstlane(bytes);
+    d[3] = 0x00020000u;
+    return d;
+}
+
+// 16 bytes per lane from a buffer straight into LDS at lds_base + 16 * lane (buffer_load_dwordx4 ... lds).
+// Written as inline asm so that the compiler's wait-count pass does not track these loads: it cannot tell one LDS
+// stage from another and would wait for every in-flight load before each LDS read.  The kernel therefore places
+// every wait on these loads itself (wait_vm before the barrier that publishes a stage).
+__device__ __forceinline__ void dma16(v4u desc, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(desc)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+    typedef const __attribute__((address_space(3))) uint8_t* lds_u8;
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8)(p));
+}
+
+// Per-wave state of the mainloop.
+struct Loader {
+    v4u rw, ra;
+    uint32_t vw[2], va[2];      // lane part of the byte offsets for even / odd instructions (OOB: share out of range)
+    uint32_t c16[2];            // 16 * logical chunk of this lane for even / odd instructions
+    uint32_t row8_w, row8_a;    // byte advance of 8 rows
+    int K;
+    int w_groups;               // SwiGLU: 8-row groups of this wave's weight share that are in range
+};
+
+// One wave's share of a stage: 8 instructions for its 64 weight rows (i = 0..7), 8 for its 64 token rows (i = 8..15).
+struct StageIssue {
+    uint32_t wdst, adst;        // LDS addresses of the wave's weight / token rows in the stage
+    uint32_t vw[2], va[2];      // byte offsets of the lane for even / odd instructions, k0 included
+};
+
+template <int EPI>
+__device__ __forceinline__ StageIssue stage_issue(uint8_t* stage, const Loader& L, int wave, int ks) {
+    StageIssue S;
+    const uint32_t k0 = (uint32_t)ks * BK;
+    const bool tail = (int)k0 + BK > L.K;                      // K tail: chunks at or past K read zeros
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const bool dead = tail && (k0 + L.c16[e]) >= (uint32_t)L.K;
+        S.vw[e] = dead ? OOB : L.vw[e] + k0;
+        S.va[e] = dead ? OOB : L.va[e] + k0;
+    }
+    S.wdst = lds_addr(stage + wave * 64 * ROWB);
+    S.adst = lds_addr(stage + A_REGION + wave * 64 * ROWB);
+    return S;
+}
+
+template <int EPI>
+__device__ __forceinline__ void issue_one(const StageIssue& S, const Loader& L, int i) {
+    if (i < 8) {
+        const uint32_t off = (EPI == EPI_SWIGLU && i >= L.w_groups) ? OOB : S.vw[i & 1] + i * L.row8_w;
+        dma16(L.rw, S.wdst + i * 8 * ROWB, off);
+    } else {
+        dma16(L.ra, S.adst + (i - 8) * 8 * ROWB, S.va[i & 1] + (i - 8) * L.row8_a);
+    }
+}
+
+template <int EPI>
+__device__ __forceinline__ void issue_stage(uint8_t* stage, const Loader& L, int wave, int ks) {
+    const StageIssue S = stage_issue<EPI>(stage, L, wave, ks);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) issue_one<EPI>(S, L, i);
+}
+
+// Weight-tile row of MFMA tile tn (0..3) of wave column wn.
+template <int EPI>
+__device__ __forceinline__ int w_tile_row(int wn, int tn) {
+    if (EPI == EPI_SWIGLU) return (tn < 2) ? (wn * 64 + 32 * tn) : (128 + wn * 64 + 32 * (tn - 2));
+    return wn * 128 + 32 * tn;
+}
+
+template <int EPI>
+__device__ __forceinline__ void read_frags(const uint8_t* stage, int wn, int wm, int lane, int sub, v8i af[4],
+                                           v8i bf[4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) af[t] = read_frag(stage + w_tile_row<EPI>(wn, t) * ROWB, lane, sub);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bf[t] = read_frag(stage + A_REGION + (wm * 128 + 32 * t) * ROWB, lane, sub);
+}
+
+// Fragment f of a sub-step: f = 0..3 weight tiles, 4..7 token tiles.
+template <int EPI>
+__device__ __forceinline__ void read_one(const uint8_t* stage, int wn, int wm, int lane, int sub, int f, v8i af[4],
+                                         v8i bf[4]) {
+    if (f < 4) af[f] = read_frag(stage + w_tile_row<EPI>(wn, f) * ROWB, lane, sub);
+    else bf[f - 4] = read_frag(stage + A_REGION + (wm * 128 + 32 * (f - 4)) * ROWB, lane, sub);
+}
+
+__device__ __forceinline__ void mfma_one(v16f acc[4][4], const v8i af[4], const v8i bf[4], int t) {
+    acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[t >> 2], bf[t & 3], acc[t >> 2][t & 3], 0, 0,
+                                                                         0, 0, 0, 0);
+}
+
+// MFMAs number lo .. hi-1 of the 16 of one sub-step (tile (i, j) = MFMA 4 i + j).
+__device__ __forceinline__ void mfma_range(v16f acc[4][4], const v8i af[4], const v8i bf[4], int lo, int hi) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+        if (t >= lo && t < hi)
+            acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[t >> 2], bf[t & 3], acc[t >> 2][t & 3],
+                                                                                 0, 0, 0, 0, 0, 0);
+}
+
+// One k-step.  On entry stage ks & 1 holds k-step ks, its sub-step-0 fragments are in f0, and the loads of k-step
+// ks+1 into the other stage are in flight.
+//   phase A: the 16 sub-step-0 MFMAs, with the reads of the 8 sub-step-1 fragments issued between the first 8;
+//   barrier 1 (after lgkmcnt(0)): every wave's reads of this stage have returned -- the stage is free;
+//   phase B: the 16 sub-step-1 MFMAs, with the 16 load instructions of k-step ks+2 into the freed stage issued two per
+//   MFMA between the first 8 (loads and reads are spread between MFMAs so that a stalled issue of a memory instruction
+//   never holds the matrix core idle), then, once this wave's share of k-step ks+1 has landed (vmcnt(16)), barrier 2
+//   publishes it and the sub-step-0 fragments of ks+1 are read between the last MFMA_SPLIT..15 MFMAs.
+// The loads of k-step ks+2 therefore have about 1.5 k-steps (about 40 MFMAs) to land.
+template <int EPI>
+__device__ __forceinline__ void kstep(uint8_t* lds, const Loader& L, int wave, int wn, int wm, int lane, int ks, int nk,
+                                      v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4], v8i fb1[4]) {
+    uint8_t* cur = lds + (ks & 1) * STAGE_BYTES;
+    uint8_t* nxt = lds + ((ks + 1) & 1) * STAGE_BYTES;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        mfma_one(acc, fa0, fb0, t);
+        if (t < 8) read_one<EPI>(cur, wn, wm, lane, 1, t, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_lgkm0();                                       // this wave's reads of stage ks & 1 have returned
+    barrier_nofence();                                  // ... and every wave's: the stage is free
+    const bool load2 = ks + 2 < nk;
+    const StageIssue S = stage_issue<EPI>(cur, L, wave, ks + 2);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        mfma_one(acc, fa1, fb1, t);
+        if (t < 8 && load2) {
+            issue_one<EPI>(S, L, 2 * t);
+            issue_one<EPI>(S, L, 2 * t + 1);
+        }
+        if (t == MFMA_SPLIT - 1 && ks + 1 < nk) {
+            if (load2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));     // k-step ks+1 landed (ks+2 may be in flight)
+            else wait_vm0();
+            barrier_nofence();
+        }
+        if (t >= MFMA_SPLIT && ks + 1 < nk) {
+            // spread the 8 fragment reads of k-step ks+1 over the MFMAs after barrier 2
+            constexpr int PER = (8 + (16 - MFMA_SPLIT) - 1) / (16 - MFMA_SPLIT);
+#pragma unroll
+            for (int f = (t - MFMA_SPLIT) * PER; f < (t - MFMA_SPLIT + 1) * PER; ++f)
+                if (f < 8) read_one<EPI>(nxt, wn, wm, lane, 0, f, fa0, fb0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 template <int OUT_DT, bool HAS_BIAS, int EPI>
-__device__ __forceinline__ void gemm_body(const GemmParams& p, int bid, uint8_t* smem) {
+__device__ __forceinline__ void gemm_body(const GemmParams& p, int bid) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE_BYTES];
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -102,208 +294,190 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int bid, uint8_t*
 
     // ---- global -> LDS addressing ----
     // lane l of an instruction covers row (l >> 3) of an 8-row group and LDS chunk (l & 7), i.e. logical chunk
-    // (l & 7) ^ (l >> 3) (the group starts at a multiple of 8 rows, so (row & 7) == (l >> 3)).
+    // (l & 7) ^ swz(row); swz depends on the row's bits 0..3, so even and odd groups of 8 rows differ.
+    Loader L;
     const uint32_t lrow = (uint32_t)(lane >> 3);
-    const uint32_t lchunk = (uint32_t)((lane & 7) ^ (lane >> 3));
+    // LDS chunk of the lane is lane & 7; its row is 8 i + lrow of the share (even i: row & 8 == 0, odd i: 8)
+    const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz((int)lrow)), (uint32_t)((lane & 7) ^ swz((int)lrow + 8))};
     int64_t wrow0;   // first global weight row of this wave's 64-row share
+    int64_t wlimit;  // rows of this share's source range (SwiGLU gate rows stop at F)
     if (EPI == EPI_SWIGLU) {
         const int f0 = tile_n * (BN / 2);
         wrow0 = (wave < 2) ? (int64_t)f0 + 64 * wave : (int64_t)p.N + f0 + 64 * (wave - 2);
+        wlimit = (wave < 2) ? (int64_t)p.N : 2 * (int64_t)p.N;
     } else {
         wrow0 = (int64_t)tile_n * BN + 64 * wave;
+        wlimit = p.N;
     }
     const int64_t arow0 = (int64_t)m0 + 64 * wave;
-    __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, p.w_bytes);
-    __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
-    // SwiGLU gate rows past F would read up rows: their groups are skipped below (F % 16 == 0 keeps groups whole).
-    const uint32_t voff_w = (uint32_t)((wrow0 + lrow) * p.ldw) + 16u * lchunk;
-    const uint32_t voff_a = (uint32_t)((arow0 + lrow) * p.lda) + 16u * lchunk;
-    const uint32_t row8_w = (uint32_t)(8 * p.ldw), row8_a = (uint32_t)(8 * p.lda);
-    // A 64-row share wholly past the end of an operand reads zeros; partial shares rely on the descriptor's range
-    // check (rows >= M or >= N start past the last valid byte).  The scalar offset is always 0 so that the range
-    // check sees the whole offset.
-    uint32_t vw = voff_w, va = voff_a;
-    const int64_t wlimit_rows = (EPI == EPI_SWIGLU) ? ((wave < 2) ? (int64_t)p.N : 2 * (int64_t)p.N) : (int64_t)p.N;
-    const int w_groups = (int)min<int64_t>(8, max<int64_t>(0, (wlimit_rows - wrow0 + 7) / 8));
-    if (wrow0 >= wlimit_rows) vw = OOB;
-    if (arow0 >= p.M) va = OOB;
-
-    const int nk = (p.K + BK - 1) / BK;
-
-    v4f acc[8][8];
+    L.rw = buffer_desc(p.w, p.w_bytes);
+    L.ra = buffer_desc(p.a, p.a_bytes);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    auto issue = [&](int ks) {
-        uint8_t* stage = smem + (ks & 1) * STAGE_BYTES;
-        const uint32_t k0 = (uint32_t)ks * BK;
-        uint32_t vwk = vw, vak = va;
-        if ((int)k0 + BK > p.K) {                           // K tail: chunks at or past K read zeros
-            const bool dead = (k0 + 16u * lchunk) >= (uint32_t)p.K;
-            vwk = dead ? OOB : vwk;
-            vak = dead ? OOB : vak;
-        }
-        uint8_t* ldw_base = stage + wave * 64 * BK;
-        uint8_t* lda_base = stage + BN * BK + wave * 64 * BK;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (EPI == EPI_SWIGLU && i >= w_groups) {
-                // gate/up rows past F: zero-fill so no up row is multiplied as a gate row
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(ldw_base + i * 8 * BK), 16, OOB, 0, 0, 0);
-            } else {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(ldw_base + i * 8 * BK), 16,
-                                                         vwk + k0 + i * row8_w, 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(lda_base + i * 8 * BK), 16,
-                                                     vak + k0 + i * row8_a, 0, 0, 0);
-    };
-
-    issue(0);
-    waitcnt_vm0();
-    __syncthreads();
-
-    const int g = lane >> 4;        // k group of the MFMA operand (32 bytes per lane)
-    const int r16 = lane & 15;
-    for (int ks = 0; ks < nk; ++ks) {
-        const uint8_t* stage = smem + (ks & 1) * STAGE_BYTES;
-        const uint8_t* wreg = stage;
-        const uint8_t* areg = stage + BN * BK;
-        // Every ds_read of this stage is issued before the next stage's LDS-DMA loads: a read issued after a DMA
-        // would make the compiler wait for that DMA (it cannot tell the two stages apart).
-        v8i bf[8], af[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) bf[j] = read_frag(areg, wm * 128 + 16 * j + r16, g);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int wr;
-            if (EPI == EPI_SWIGLU) wr = (i < 4) ? (wn * 64 + 16 * i + r16) : (128 + wn * 64 + 16 * (i - 4) + r16);
-            else wr = wn * 128 + 16 * i + r16;
-            af[i] = read_frag(wreg, wr, g);
-        }
-        if (ks + 1 < nk) issue(ks + 1);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bf[j], acc[i][j], 0, 0, 0, 0, 0, 0);
-        // keep the wait for the next stage behind this stage's MFMAs (the scheduler would hoist it otherwise)
-        __builtin_amdgcn_sched_barrier(0);
-        waitcnt_vm0();
-        waitcnt_lgkm0();
-        __syncthreads();
+    for (int e = 0; e < 2; ++e) {
+        L.c16[e] = 16u * lch[e];
+        L.vw[e] = (wrow0 >= wlimit) ? OOB : (uint32_t)((wrow0 + lrow) * p.ldw) + L.c16[e];
+        L.va[e] = (arow0 >= p.M) ? OOB : (uint32_t)((arow0 + lrow) * p.lda) + L.c16[e];
     }
+    L.row8_w = (uint32_t)(8 * p.ldw);
+    L.row8_a = (uint32_t)(8 * p.lda);
+    L.K = p.K;
+    // Partial shares rely on the descriptor's range check (rows >= M or >= N start past the last valid byte), except
+    // SwiGLU gate rows past F, which would read up rows: those 8-row groups are zero-filled (F % 16 == 0).
+    L.w_groups = (int)min<int64_t>(8, max<int64_t>(0, (wlimit - wrow0 + 7) / 8));
+
+    const int nk = (p.K + BK - 1) / BK;             // k-steps of 128
+
+    v16f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // prologue: k-steps 0 and 1 in flight, the sub-step-0 fragments of k-step 0 in registers
+    v8i fa0[4], fb0[4], fa1[4], fb1[4];
+    issue_stage<EPI>(lds, L, wave, 0);
+    if (nk > 1) {
+        issue_stage<EPI>(lds + STAGE_BYTES, L, wave, 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));
+    } else {
+        wait_vm0();
+    }
+    barrier_nofence();
+    read_frags<EPI>(lds, wn, wm, lane, 0, fa0, fb0);
+    for (int ks = 0; ks < nk; ++ks) kstep<EPI>(lds, L, wave, wn, wm, lane, ks, nk, acc, fa0, fb0, fa1, fb1);
 
     // ---- epilogue ----
-    const int q4 = lane >> 4;       // which 4 consecutive channels of the 16-wide MFMA tile
+    // The scaled, rounded outputs go through LDS so that global stores are whole 16-byte pieces of contiguous row
+    // segments (a wave's 128 x 128 tile leaves the MFMA layout with only 8 contiguous bytes per lane and row).
+    // 32x32 MFMA result: lane l, register 4q + r holds D[8q + 4(l >> 5) + r][l & 31], i.e. channel
+    // n = tile_n_base + 8q + 4(l >> 5) + r of token m = tile_m_base + (l & 31).
+    wait_lgkm0();
+    barrier_nofence();                                  // every wave is done with the stages: reuse the LDS
+    constexpr int OUT_COLS = (EPI == EPI_SWIGLU) ? 64 : 128;   // output columns per wave
+    constexpr int ROW_BYTES = OUT_COLS * 2;
+    constexpr int CHUNKS = ROW_BYTES / 16;                       // 16-byte chunks per row: 16 or 8
+    uint8_t* tile = lds + wave * (128 * ROW_BYTES);
+    // element (ml, cl) of the wave tile: row ml, 16-byte chunk (cl / 8) ^ (ml % CHUNKS), 8-byte half (cl / 4) % 2
+    auto put4 = [&](int ml, int cl, uint32_t lo, uint32_t hi2) {
+        const int ch = (cl >> 3) ^ (ml & (CHUNKS - 1));
+        *reinterpret_cast<uint2*>(tile + ml * ROW_BYTES + ch * 16 + ((cl >> 2) & 1) * 8) = make_uint2(lo, hi2);
+    };
+    const int hi = lane >> 5;
+    const int mj = lane & 31;
+    const int mrow0 = m0 + wm * 128;
+    uint32_t rmax[4] = {0, 0, 0, 0};
+    float sam[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = mrow0 + 32 * j + mj;
+        sam[j] = (m < p.M) ? p.sa[(int64_t)m * p.sa_stride] : 0.0f;
+    }
+    int col0, ncols;                                    // first output column of the wave, output width
     if (EPI == EPI_SWIGLU) {
         const int F = p.N;
-        const int fbase = tile_n * (BN / 2) + wn * 64;
-        uint32_t rmax[8];
+        col0 = tile_n * (BN / 2) + wn * 64;
+        ncols = F;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) rmax[j] = 0;
+        for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int f = fbase + 16 * i + 4 * q4;
-            if (f >= F) continue;
-            float sbg[4], sbu[4], bg[4] = {0, 0, 0, 0}, bu[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sbg[r] = p.sb[(int64_t)(f + r) * p.sb_stride];
-                sbu[r] = p.sb[(int64_t)(F + f + r) * p.sb_stride];
-                if (HAS_BIAS) { bg[r] = load_bias(p.bias, f + r, 0); bu[r] = load_bias(p.bias, F + f + r, 0); }
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int m = m0 + wm * 128 + 16 * j + r16;
-                if (m >= p.M) continue;
-                const float sam = p.sa[(int64_t)m * p.sa_stride];
-                uint32_t hb[4];
+            for (int q = 0; q < 4; ++q) {
+                const int cl = 32 * t + 8 * q + 4 * hi;
+                const int f = col0 + cl;
+                const bool fok = f < F;
+                float sbg[4], sbu[4], bg[4] = {0, 0, 0, 0}, bu[4] = {0, 0, 0, 0};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float tg = sbg[r] * acc[i][j][r];
-                    const float tu = sbu[r] * acc[i + 4][j][r];
-                    const float gy = HAS_BIAS ? __builtin_fmaf(sam, tg, bg[r]) : sam * tg;
-                    const float uy = HAS_BIAS ? __builtin_fmaf(sam, tu, bu[r]) : sam * tu;
-                    const uint32_t gb = bf16_rne(gy);
-                    float u = bf16_to_f32(bf16_rne(uy));
-                    u = (u == 0.0f) ? 0.0f : u;                       // -0 up -> +0 (fp8_swiglu.py:66)
-                    const float s = bf16_to_f32(p.silu[gb]);
-                    hb[r] = bf16_rne(s * u);
-                    const uint32_t ab = (hb[r] & 0x7fffu) << 16;
-                    rmax[j] = rmax[j] > ab ? rmax[j] : ab;
+                    sbg[r] = fok ? p.sb[(int64_t)(f + r) * p.sb_stride] : 0.0f;
+                    sbu[r] = fok ? p.sb[(int64_t)(F + f + r) * p.sb_stride] : 0.0f;
+                    if (HAS_BIAS && fok) { bg[r] = load_bias(p.bias, f + r, 0); bu[r] = load_bias(p.bias, F + f + r, 0); }
                 }
-                uint2 v = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * p.ldy + f) = v;
-            }
-        }
-        if (p.row_amax) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                uint32_t v = rmax[j];
-                uint32_t o = (uint32_t)__shfl_xor((int)v, 16, 64); v = v > o ? v : o;
-                o = (uint32_t)__shfl_xor((int)v, 32, 64); v = v > o ? v : o;
-                const int m = m0 + wm * 128 + 16 * j + r16;
-                if (q4 == 0 && m < p.M && v) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, v);
-            }
-        }
-        return;
-    }
-
-    const int nbase = tile_n * BN + wn * 128;
-    uint32_t rmax[8];
+                for (int j = 0; j < 4; ++j) {
+                    const bool ok = fok && (mrow0 + 32 * j + mj < p.M);
+                    uint32_t hb[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) rmax[j] = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int n = nbase + 16 * i + 4 * q4;
-        if (n >= p.N) continue;
-        float sbn[4], bn[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sbn[r] = p.sb[(int64_t)(n + r) * p.sb_stride];
-            if (HAS_BIAS) bn[r] = load_bias(p.bias, n + r, OUT_DT);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int m = m0 + wm * 128 + 16 * j + r16;
-            if (m >= p.M) continue;
-            const float sam = p.sa[(int64_t)m * p.sa_stride];
-            uint32_t o[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float t = sbn[r] * acc[i][j][r];
-                const float v = HAS_BIAS ? __builtin_fmaf(sam, t, bn[r]) : sam * t;
-                o[r] = OUT_DT ? fp16_rne(v) : bf16_rne(v);
-                if (EPI == EPI_AMAX) {
-                    const uint32_t ab = (o[r] & 0x7fffu) << 16;
-                    rmax[j] = rmax[j] > ab ? rmax[j] : ab;
+                    for (int r = 0; r < 4; ++r) {
+                        const float tg = sbg[r] * acc[t][j][4 * q + r];
+                        const float tu = sbu[r] * acc[t + 2][j][4 * q + r];
+                        const float gy = HAS_BIAS ? __builtin_fmaf(sam[j], tg, bg[r]) : sam[j] * tg;
+                        const float uy = HAS_BIAS ? __builtin_fmaf(sam[j], tu, bu[r]) : sam[j] * tu;
+                        const uint32_t gb = bf16_rne(gy);
+                        float u = bf16_to_f32(bf16_rne(uy));
+                        u = (u == 0.0f) ? 0.0f : u;                       // -0 up -> +0 (fp8_swiglu.py:66)
+                        const float sl = bf16_to_f32(p.silu[gb]);
+                        hb[r] = bf16_rne(sl * u);
+                        const uint32_t ab = ok ? ((hb[r] & 0x7fffu) << 16) : 0u;
+                        rmax[j] = rmax[j] > ab ? rmax[j] : ab;
+                    }
+                    put4(32 * j + mj, cl, hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
                 }
             }
-            uint2 v = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * p.ldy + n) = v;
+        }
+    } else {
+        col0 = tile_n * BN + wn * 128;
+        ncols = p.N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int cl = 32 * i + 8 * q + 4 * hi;
+                const int n = col0 + cl;
+                const bool nok = n < p.N;
+                float sbn[4], bn[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sbn[r] = nok ? p.sb[(int64_t)(n + r) * p.sb_stride] : 0.0f;
+                    if (HAS_BIAS && nok) bn[r] = load_bias(p.bias, n + r, OUT_DT);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool ok = nok && (mrow0 + 32 * j + mj < p.M);
+                    uint32_t o[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float t = sbn[r] * acc[i][j][4 * q + r];
+                        const float v = HAS_BIAS ? __builtin_fmaf(sam[j], t, bn[r]) : sam[j] * t;
+                        o[r] = OUT_DT ? fp16_rne(v) : bf16_rne(v);
+                        if (EPI == EPI_AMAX) {
+                            const uint32_t ab = ok ? ((o[r] & 0x7fffu) << 16) : 0u;
+                            rmax[j] = rmax[j] > ab ? rmax[j] : ab;
+                        }
+                    }
+                    put4(32 * j + mj, cl, o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+                }
+            }
         }
     }
-    if (EPI == EPI_AMAX) {
+    if (EPI == EPI_AMAX || (EPI == EPI_SWIGLU && p.row_amax)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 4; ++j) {
             uint32_t v = rmax[j];
-            uint32_t o = (uint32_t)__shfl_xor((int)v, 16, 64); v = v > o ? v : o;
-            o = (uint32_t)__shfl_xor((int)v, 32, 64); v = v > o ? v : o;
-            const int m = m0 + wm * 128 + 16 * j + r16;
-            if (q4 == 0 && m < p.M && v) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, v);
+            const uint32_t o = (uint32_t)__shfl_xor((int)v, 32, 64);
+            v = v > o ? v : o;
+            const int m = mrow0 + 32 * j + mj;
+            if (hi == 0 && m < p.M && v) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, v);
         }
+    }
+    // the wave reads back its own tile (LDS accesses of one wave complete in order): 16 bytes per lane, CHUNKS lanes
+    // per row, whole row segments per store instruction
+    constexpr int ROWS_PER_PASS = 64 / CHUNKS;
+    const int c = lane % CHUNKS;
+    const int col = col0 + c * 8;
+    uint16_t* ybase = reinterpret_cast<uint16_t*>(p.y);
+#pragma unroll 4
+    for (int it = 0; it < 128 / ROWS_PER_PASS; ++it) {
+        const int ml = it * ROWS_PER_PASS + lane / CHUNKS;
+        const uint4 v = *reinterpret_cast<const uint4*>(tile + ml * ROW_BYTES + ((c ^ (ml & (CHUNKS - 1))) << 4));
+        const int m = mrow0 + ml;
+        if (m < p.M && col < ncols) *reinterpret_cast<uint4*>(ybase + (int64_t)m * p.ldy + col) = v;
     }
 }
 
 template <int OUT_DT, bool HAS_BIAS, int EPI>
 __global__ void __launch_bounds__(256, 1) gemm_kernel(GemmParams p) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-    gemm_body<OUT_DT, HAS_BIAS, EPI>(p, (int)blockIdx.x, smem);
+    gemm_body<OUT_DT, HAS_BIAS, EPI>(p, (int)blockIdx.x);
 }
 
 struct GroupedParams {
@@ -313,13 +487,12 @@ struct GroupedParams {
 
 // One launch over the concatenated tile spaces of up to H3FP8_MAX_GROUPS problems (bf16 out, no bias).
 __global__ void __launch_bounds__(256, 1) gemm_grouped_kernel(GroupedParams gp) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int b = (int)blockIdx.x;
     int i = 0;
 #pragma unroll
     for (int j = 1; j < H3FP8_MAX_GROUPS; ++j)
         if (j < gp.n && b >= gp.g[j].tile_offset) i = j;
-    gemm_body<0, false, EPI_PLAIN>(gp.g[i], b - gp.g[i].tile_offset, smem);
+    gemm_body<0, false, EPI_PLAIN>(gp.g[i], b - gp.g[i].tile_offset);
 }
 
 __global__ void __launch_bounds__(256) fill_zero_kernel(float* p, int64_t n) {
@@ -334,24 +507,9 @@ int zero_rows(float* p, int64_t n, hipStream_t st) {
     return H3FP8_OK;
 }
 
-// Raises a kernel's dynamic-LDS limit to LDS_BYTES once per device.
-int allow_lds(const void* fn, bool* done) {
-    int dev = 0;
-    H3_CHECK_HIP(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) return H3FP8_EINVAL;
-    if (!done[dev]) {
-        H3_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
-        done[dev] = true;
-    }
-    return H3FP8_OK;
-}
-
 template <int OUT_DT, bool HAS_BIAS, int EPI>
 int launch_one(const GemmParams& p, int blocks, hipStream_t st) {
-    static bool done[64] = {};
-    int rc = allow_lds((const void*)gemm_kernel<OUT_DT, HAS_BIAS, EPI>, done);
-    if (rc) return rc;
-    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI>), dim3(blocks), dim3(256), LDS_BYTES, st, p);
+    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI>), dim3(blocks), dim3(256), 0, st, p);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
@@ -510,10 +668,7 @@ int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream) {
         gp.g[gp.n++] = p;
     }
     if (blocks == 0) return H3FP8_OK;
-    static bool done[64] = {};
-    int rc = allow_lds((const void*)gemm_grouped_kernel, done);
-    if (rc) return rc;
-    hipLaunchKernelGGL(gemm_grouped_kernel, dim3(blocks), dim3(256), LDS_BYTES, (hipStream_t)stream, gp);
+    hipLaunchKernelGGL(gemm_grouped_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, gp);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }

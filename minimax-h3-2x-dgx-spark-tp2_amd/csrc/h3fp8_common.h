@@ -35,8 +35,11 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
     return ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : r;
 }
 
-// fp32 -> fp16 bits, round to nearest even (hardware cvt: IEEE RNE, overflow -> inf, denormals kept).
+// fp32 -> fp16 bits, round to nearest even (hardware cvt: IEEE RNE, overflow -> inf, denormals kept).  The value is
+// first pinned as an fp32 register: otherwise the compiler folds the producing fp32 multiply into v_fma_mix*_f16,
+// which rounds the exact product once to fp16 instead of rounding to fp32 and then to fp16 as the reference does.
 __device__ __forceinline__ uint32_t fp16_rne(float f) {
+    asm("" : "+v"(f));
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 

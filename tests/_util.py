@@ -72,3 +72,33 @@ def ref_gemm(a: torch.Tensor, w: torch.Tensor, sa, sb, bias=None, out_fp16=False
     sb_n = f32(sb).reshape(-1)
     b = None if bias is None else bits16(bias)
     return O.epilogue(acc, sa_n, sb_n, b, out_fp16)
+
+
+def bf16_from_bits(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def check_close_bf16(y: torch.Tensor, ref_bits: np.ndarray, min_equal: float = 0.95, row_frac: float = 2.0 ** -10,
+                     ulps: float = 1.0):
+    """Tolerance for a bf16 GEMM output against the oracle (fp32-accumulated dequantised product, same epilogue).
+
+    The kernel and the oracle sum K in different orders, so their fp32 accumulators differ by a few fp32 ulps and a
+    bf16 rounding may flip.  Stated bound, per element:  |y - ref| <= ulp_bf16(ref) + 2^-10 * rms(row of ref)
+    (one bf16 ulp, plus an absolute slack for cancellation near zero), and at least ``min_equal`` of the outputs
+    bit-equal.  Returns (max |err| / rms, fraction bit-equal).  The whole-tensor form "max |err| <= 2e-2 * rms" is not
+    used: one ulp at |y| > 5 rms already exceeds it for bf16 outputs."""
+    out = f32(y).astype(np.float64)
+    ref = bf16_from_bits(ref_bits).astype(np.float64)
+    assert np.isfinite(out).all() and np.isfinite(ref).all()
+    mag = np.abs(ref)
+    e = np.floor(np.log2(np.where(mag > 0, mag, 1.0)))
+    ulp = np.where(mag > 0, np.exp2(e - 7), 0.0)
+    row_rms = np.sqrt(np.mean(ref * ref, axis=1, keepdims=True))
+    err = np.abs(out - ref)
+    bound = ulps * ulp + row_frac * row_rms
+    bad = err > bound
+    assert not bad.any(), f"{int(bad.sum())} outputs beyond {ulps} ulp + {row_frac} rms_row; worst {np.max(err - bound)}"
+    eq = float(np.mean(bits16(y) == ref_bits))
+    assert eq >= min_equal, eq
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    return float(err.max()) / rms, eq

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import assert_quant_equal, bits16, bits8, f32, int_operands, serving_like
+from _util import assert_quant_equal, bits16, bits8, check_close_bf16, f32, int_operands, serving_like
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -96,16 +96,14 @@ def test_gemm_swiglu_integer_exact(cuda, M, F, K, bias):
 
 @pytest.mark.parametrize("M", [200, 1000])
 def test_gemm_swiglu_random_within_tolerance(cuda, M):
-    """Serving-like fc1 operands: the fused kernel vs the oracle's SwiGLU of the fp32 product; the SwiGLU output is
-    within 2e-2 * rms and >= 95 % bit-equal (accumulation order only)."""
+    """Serving-like fc1 operands: the fused kernel vs the oracle's SwiGLU of the fp32 product, within the GEMM
+    tolerance form (_util.check_close_bf16) widened to 2 bf16 ulps + 2^-6 rms_row: a flipped gate rounding moves
+    silu(g) by up to |silu'(g)| ulp(g), several ulps of s where |s| << |g|; a flipped gate or up rounding
+    moves h by up to about two ulps; >= 95 % bit-equal."""
     from h3_tp2_amd import ops
     F, K = 4096, 5376
     a, w, sa, sb = serving_like(M, 2 * F, K, seed=M + 17, device=cuda)
     h = ops.gemm_swiglu(a, w, sa, sb)
     torch.cuda.synchronize()
     h_ref = O.scale_swiglu(O.matmul_f32(bits8(a), bits8(w)), f32(sa), f32(sb))
-    ref = torch.from_numpy(h_ref.view(np.int16)).view(torch.bfloat16).float().numpy()
-    out = f32(h)
-    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
-    assert float(np.max(np.abs(out - ref))) <= 2e-2 * rms
-    assert float(np.mean(bits16(h) == h_ref)) >= 0.95
+    check_close_bf16(h, h_ref, row_frac=2.0 ** -6, ulps=2.0)
