@@ -1,0 +1,271 @@
+"""Benchmark of the online-FP8 DiT linear path on one MI355X: prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only WORKLOAD]
+
+Headline workload (``value``): the QKV projection at the 5 s 960x576 token count -- X bf16 [16740, 3072] quantised
+per token to e4m3fn (kernel 1), then the scaled FP8 GEMM against the per-channel-quantised QKV weight [9216, 3072]
+with a bf16 output (kernel 2).  A step is one quant + one GEMM over the whole token sequence, inputs resident in HBM;
+``value`` = 2 M N K / (step time) in TFLOP/s.  ``roofline`` is the GEMM kernel alone against the FP8 dense MFMA peak
+(5.0 PFLOP/s), its average launch time measured with HIP events on the launch stream.  The other measured workloads
+(the single linear, the fused FFN and the 15 s block chain at 1344x768, the grouped launch, and the quant / SwiGLU-tail
+passes against the 8 TB/s HBM peak) are reported under ``workloads``.  ``cpu_baseline`` times the CPU oracle of the
+reference's torch CPU path (per-token quant, fp32 product, scaled epilogue) on a row slice of the headline workload on
+this host's cores, scaled to the full token count.  Synthetic seeded inputs, random-init weights (no checkpoints).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "minimax-h3-2x-dgx-spark-tp2_amd"))
+
+METRIC = "FP8 DiT-linear TFLOP/s (% FP8 MFMA peak) + quant/SwiGLU HBM GB/s"
+PEAK_TFLOPS = 5000.0          # MI355X dense FP8 MFMA
+PEAK_GBS = 8000.0             # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
+    ap.add_argument("--cpu-rows", type=int, default=8192, help="token rows of the CPU baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 512 MiB device-to-device copy (the known-size kernel that scales PMC byte counts)")
+    return ap.parse_args()
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs the online-FP8 path on one GPU only (the full token sequence resident, no "
+              "sharding, no collectives); --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from h3_tp2_amd import ops, synthetic
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    ops.init(0)
+    stream = torch.cuda.current_stream(dev)
+    only = set(filter(None, args.only.split(",")))
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    def time_steps(fn, steps, warmup):
+        """Total time of `steps` back-to-back calls (ms), after `warmup` untimed ones; synchronised on both sides."""
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        s, e = ev(), ev()
+        s.record(stream)
+        for _ in range(steps):
+            fn()
+        e.record(stream)
+        e.synchronize()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e)
+
+    def quantised_weight(N, K, seed):
+        w, sw = ops.quant_rows(synthetic.weight(N, K, seed).to(dev))
+        return w, sw.view(-1)
+
+    out = {}
+
+    if args.copy_calibration:
+        src = torch.empty(512 << 20, device=dev, dtype=torch.uint8).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    # ---- headline: QKV projection, 960x576 5 s (M = 31 x 540) ----
+    c2 = synthetic.CONFIGS["c2_qkv_960x576_5s"]
+    M, K, N = c2["M"], c2["K"], c2["N"]
+    x = synthetic.activations(M, K, seed=0, n_out=c2["n_out"]).to(dev)
+    w, sw = quantised_weight(N, K, seed=1)
+    q = torch.empty((M, K), device=dev, dtype=ops.E4M3)
+    sq = torch.empty((M, 1), device=dev, dtype=torch.float32)
+    y = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+
+    def qkv_step():
+        ops.quant_rows(x, q, sq)
+        ops.gemm(q, w, sq, sw, torch.bfloat16, out=y)
+
+    steps, warm = args.steps, args.warmup
+    t_step = time_steps(qkv_step, steps, warm) / steps
+    flops = 2.0 * M * N * K
+    t_gemm = time_steps(lambda: ops.gemm(q, w, sq, sw, torch.bfloat16, out=y), steps, warm) / steps
+    t_quant = time_steps(lambda: ops.quant_rows(x, q, sq), steps, warm) / steps
+    value = flops / (t_step * 1e-3) / 1e12
+    gemm_tf = flops / (t_gemm * 1e-3) / 1e12
+    quant_bytes = 3.0 * M * K + 4.0 * M
+    out["qkv_quant"] = {"ms": round(t_quant, 4), "GB/s": round(quant_bytes / (t_quant * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(quant_bytes / (t_quant * 1e-3) / 1e9 / PEAK_GBS, 4)}
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemm_qkv_960x576_traffic.txt")
+    if os.path.exists(tpath):
+        for line in open(tpath):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = float(line.split(":", 1)[1])
+
+    roofline = {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(gemm_tf / PEAK_TFLOPS, 4), "traffic": traffic,
+                "kernel": "gemm_kernel<bf16> (kernel 2)", "launch_ms": round(t_gemm, 4),
+                "flops_per_launch": flops}
+    del x
+
+    # ---- the other measured workloads ----
+    def want(name):
+        return not only or name in only
+
+    if want("c1"):
+        c = synthetic.CONFIGS["c1_single_linear"]
+        M1, K1, N1 = c["M"], c["K"], c["N"]
+        x1 = synthetic.activations(M1, K1, seed=0, n_out=c["n_out"]).to(dev)
+        w1, s1 = quantised_weight(N1, K1, seed=1)
+        q1 = torch.empty((M1, K1), device=dev, dtype=ops.E4M3)
+        sq1 = torch.empty((M1, 1), device=dev, dtype=torch.float32)
+        y1 = torch.empty((M1, N1), device=dev, dtype=torch.bfloat16)
+
+        def c1_step():
+            ops.quant_rows(x1, q1, sq1)
+            ops.gemm(q1, w1, sq1, s1, torch.bfloat16, out=y1)
+        t = time_steps(c1_step, steps, warm) / steps
+        out["c1_single_linear_2048x3072x3072"] = {"ms": round(t, 4),
+                                                 "TFLOP/s": round(2.0 * M1 * N1 * K1 / (t * 1e-3) / 1e12, 1)}
+        del x1, w1, q1, y1
+
+    if want("c3"):
+        c = synthetic.CONFIGS["c3_ffn_1344x768_5s"]
+        M3, K3, F3 = c["M"], c["K"], c["F"]
+        x3 = synthetic.activations(M3, K3, seed=0, n_out=c["n_out"]).to(dev)
+        wgu, sgu = quantised_weight(2 * F3, K3, seed=2)
+        wd, sd = quantised_weight(K3, F3, seed=3)
+        q3 = torch.empty((M3, K3), device=dev, dtype=ops.E4M3)
+        sq3 = torch.empty((M3, 1), device=dev, dtype=torch.float32)
+        hws = torch.empty((M3, F3), device=dev, dtype=torch.bfloat16)
+        y3 = torch.empty((M3, K3), device=dev, dtype=torch.bfloat16)
+
+        def c3_step():
+            ops.quant_rows(x3, q3, sq3)
+            qh, sh = ops.gemm_swiglu_quant(q3, wgu, sq3, sgu, h_ws=hws)
+            ops.gemm(qh, wd, sh, sd, torch.bfloat16, out=y3)
+        t = time_steps(c3_step, steps, warm) / steps
+        f3 = 2.0 * M3 * (2 * F3) * K3 + 2.0 * M3 * K3 * F3
+        t_gu = time_steps(lambda: ops.gemm_swiglu(q3, wgu, sq3, sgu), steps, warm) / steps
+        amax = torch.empty((M3,), device=dev, dtype=torch.float32)
+        ops.gemm_swiglu(q3, wgu, sq3, sgu, row_amax=amax)
+        hq = torch.empty((M3, F3), device=dev, dtype=ops.E4M3)
+        hs = torch.empty((M3, 1), device=dev, dtype=torch.float32)
+        h_in = ops.gemm_swiglu(q3, wgu, sq3, sgu)
+        t_tail = time_steps(lambda: ops.quant_rows_amax(h_in, amax, hq, hs), steps, warm) / steps
+        tail_bytes = 3.0 * M3 * F3 + 4.0 * M3
+        gu_in = torch.empty((M3, 2 * F3), device=dev, dtype=torch.bfloat16).normal_()
+        t_sq = time_steps(lambda: ops.silu_mul_quant(gu_in), steps, warm) / steps
+        sq_bytes = 5.0 * M3 * F3 + 4.0 * M3
+        out["c3_ffn_1344x768_5s"] = {
+            "ms": round(t, 4), "TFLOP/s": round(f3 / (t * 1e-3) / 1e12, 1),
+            "gate_up_swiglu_TFLOP/s": round(2.0 * M3 * 2 * F3 * K3 / (t_gu * 1e-3) / 1e12, 1),
+            "swiglu_requant_tail": {"form": "tail pass of the fused epilogue (3 M F + 4 M bytes)",
+                                    "GB/s": round(tail_bytes / (t_tail * 1e-3) / 1e9, 1),
+                                    "frac_hbm": round(tail_bytes / (t_tail * 1e-3) / 1e9 / PEAK_GBS, 4)},
+            "swiglu_requant_standalone": {"form": "bf16 [M, 2F] -> e4m3 [M, F] (5 M F + 4 M bytes)",
+                                          "GB/s": round(sq_bytes / (t_sq * 1e-3) / 1e9, 1),
+                                          "frac_hbm": round(sq_bytes / (t_sq * 1e-3) / 1e9 / PEAK_GBS, 4)}}
+        del x3, wgu, wd, q3, hws, y3, h_in, gu_in, hq
+
+    if want("c4"):
+        c = synthetic.CONFIGS["c4_chain_1344x768_15s"]
+        M4, K4 = c["M"], c["K"]
+        F4 = 8192
+        x4 = synthetic.activations(M4, K4, seed=0, n_out=c["n_out"]).to(dev)
+        xo = synthetic.activations(M4, K4, seed=5, n_out=c["n_out"]).to(dev)   # attention output stand-in
+        wqkv, sqkv = quantised_weight(3 * K4, K4, seed=1)
+        wo, so = quantised_weight(K4, K4, seed=4)
+        wgu, sgu = quantised_weight(2 * F4, K4, seed=2)
+        wd, sd = quantised_weight(K4, F4, seed=3)
+        q4 = torch.empty((M4, K4), device=dev, dtype=ops.E4M3)
+        s4 = torch.empty((M4, 1), device=dev, dtype=torch.float32)
+        yqkv = torch.empty((M4, 3 * K4), device=dev, dtype=torch.bfloat16)
+        hws = torch.empty((M4, F4), device=dev, dtype=torch.bfloat16)
+
+        def c4_step():
+            ops.quant_rows(x4, q4, s4)                                       # block input -> fp8
+            ops.gemm(q4, wqkv, s4, sqkv, torch.bfloat16, out=yqkv)           # QKV (to attention)
+            qo, so_ = ops.quant_rows(xo)                                     # attention output -> fp8
+            _, qg, sg = ops.gemm_quant(qo, wo, so_, so)                      # out-proj + fused quant
+            qh, sh = ops.gemm_swiglu_quant(qg, wgu, sg, sgu, h_ws=hws)       # gate/up + SwiGLU + requant
+            ops.gemm_quant(qh, wd, sh, sd)                                   # down + next block's quant
+        t = time_steps(c4_step, max(2, steps // 4), max(1, warm // 2)) / max(2, steps // 4)
+        f4 = 2.0 * M4 * (3 * K4 * K4 + K4 * K4 + 2 * F4 * K4 + K4 * F4)
+        t_q = time_steps(lambda: ops.quant_rows(x4, q4, s4), steps, warm) / steps
+        qb = 3.0 * M4 * K4 + 4.0 * M4
+        out["c4_chain_1344x768_15s"] = {"ms": round(t, 3), "TFLOP/s": round(f4 / (t * 1e-3) / 1e12, 1),
+                                        "quant_3072": {"GB/s": round(qb / (t_q * 1e-3) / 1e9, 1),
+                                                       "frac_hbm": round(qb / (t_q * 1e-3) / 1e9 / PEAK_GBS, 4)},
+                                        "note": "out-proj input is a seeded bf16 stand-in for the attention output"}
+        del x4, xo, wqkv, wo, wgu, wd, q4, yqkv, hws
+
+    if want("c5"):
+        groups = synthetic.CONFIGS["c5_grouped"]["groups"]
+        probs, xs = [], []
+        for i, (Mg, Kg, Ng, no) in enumerate(groups):
+            xg = synthetic.activations(Mg, Kg, seed=10 + i, n_out=no).to(dev)
+            wg, sg = quantised_weight(Ng, Kg, seed=20 + i)
+            qg, sqg = ops.quant_rows(xg)
+            probs.append((qg, wg, sqg, sg))
+            xs.append(xg)
+        t = time_steps(lambda: ops.grouped_gemm(probs), steps, warm) / steps
+        f5 = sum(2.0 * Mg * Ng * Kg for Mg, Kg, Ng, _ in groups)
+        out["c5_grouped_one_launch"] = {"ms": round(t, 4), "TFLOP/s": round(f5 / (t * 1e-3) / 1e12, 1)}
+        del probs, xs
+
+    # ---- CPU baseline: the oracle of the reference's torch CPU path on a row slice of the headline workload ----
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, ROOT)
+        import numpy as np
+
+        from oracle import oracle as O
+        rows = min(args.cpu_rows, M)
+        xs = synthetic.activations(M, K, seed=0, n_out=c2["n_out"])[:rows]
+        xb = xs.view(torch.int16).numpy().view(np.uint16)
+        wb = synthetic.weight(N, K, seed=1).view(torch.int16).numpy().view(np.uint16)
+        wq, swq = O.quant_rows(wb)
+        O.linear(xb[:16], wq, swq)                                           # warm-up
+        best = None
+        for _ in range(2):
+            t0 = time.perf_counter()
+            O.linear(xb, wq, swq)
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        t_full = best * M / rows
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        cpu = {"value": round(flops / t_full / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": f"oracle per-token quant + numpy fp32 product + C epilogue on {rows} of {M} token rows "
+                         f"(min of 2 runs, {best:.2f} s), scaled linearly to {M} rows",
+               "host_cpu_count": os.cpu_count()}
+
+    line = {"metric": METRIC, "value": round(value, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+            "warmup": warm, "ms_per_step": round(t_step, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "e4m3", "data": "synthetic (seeded N(0,1) activations with x40 outlier "
+            "channels, random-init N(0,0.02) weights)",
+            "config": {"workload": "qkv_960x576_5s: quant X[16740,3072] + FP8 GEMM vs W[9216,3072], bf16 out",
+                       "M": M, "K": K, "N": N, "parallelism": "single GPU"},
+            "roofline": roofline, "cpu_baseline": cpu, "workloads": out}
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -353,6 +353,25 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int bid) {
     // segments (a wave's 128 x 128 tile leaves the MFMA layout with only 8 contiguous bytes per lane and row).
     // 32x32 MFMA result: lane l, register 4q + r holds D[8q + 4(l >> 5) + r][l & 31], i.e. channel
     // n = tile_n_base + 8q + 4(l >> 5) + r of token m = tile_m_base + (l & 31).
+    if (OUT_DT == H3FP8_DT_F32) {
+        // probe mode: the raw fp32 accumulators, scales / bias / rounding not applied (16-byte stores per lane)
+        float* yf = reinterpret_cast<float*>(p.y);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = tile_n * BN + wn * 128 + 32 * i + 8 * q + 4 * (lane >> 5);
+                    const int m = m0 + wm * 128 + 32 * j + (lane & 31);
+                    if (n < p.N && m < p.M) {
+                        const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                       acc[i][j][4 * q + 3]};
+                        *reinterpret_cast<v4f*>(yf + (int64_t)m * p.ldy + n) = v;
+                    }
+                }
+        return;
+    }
     wait_lgkm0();
     barrier_nofence();                                  // every wave is done with the stages: reuse the LDS
     constexpr int OUT_COLS = (EPI == EPI_SWIGLU) ? 64 : 128;   // output columns per wave
@@ -519,6 +538,7 @@ int dispatch(const GemmParams& p, int out_dt, bool has_bias, int blocks, hipStre
     if (out_dt == H3FP8_DT_BF16) {
         return has_bias ? launch_one<0, true, EPI>(p, blocks, st) : launch_one<0, false, EPI>(p, blocks, st);
     }
+    if (out_dt == H3FP8_DT_F32) return launch_one<H3FP8_DT_F32, false, EPI_PLAIN>(p, blocks, st);
     return has_bias ? launch_one<1, true, EPI>(p, blocks, st) : launch_one<1, false, EPI>(p, blocks, st);
 }
 
@@ -599,7 +619,10 @@ int h3fp8_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const flo
                int64_t N, int64_t K, float* row_amax, void* stream) {
     int rc = check_gemm(a, lda, w, ldw, sa, sa_stride, sb, sb_stride, y, ldy, M, N, K, N, "h3fp8_gemm");
     if (rc) return rc;
-    H3_REQUIRE(out_dtype == H3FP8_DT_BF16 || out_dtype == H3FP8_DT_FP16, "h3fp8_gemm: bad out_dtype %d", out_dtype);
+    H3_REQUIRE(out_dtype == H3FP8_DT_BF16 || out_dtype == H3FP8_DT_FP16 || out_dtype == H3FP8_DT_F32,
+               "h3fp8_gemm: bad out_dtype %d", out_dtype);
+    H3_REQUIRE(out_dtype != H3FP8_DT_F32 || (!bias && !row_amax && ldy % 4 == 0),
+               "h3fp8_gemm: the fp32 accumulator probe takes no bias or row_amax and needs ldy %% 4 == 0");
     if (M == 0 || N == 0) return H3FP8_OK;
     hipStream_t st = (hipStream_t)stream;
     if (row_amax) {

@@ -15,6 +15,7 @@ ABI_VERSION = 1
 
 H3FP8_DT_BF16 = 0
 H3FP8_DT_FP16 = 1
+H3FP8_DT_F32 = 2
 MAX_GROUPS = 8
 
 _lib = None

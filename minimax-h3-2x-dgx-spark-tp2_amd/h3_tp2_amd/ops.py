@@ -19,7 +19,7 @@ E4M3 = torch.float8_e4m3fn
 FP8_MAX = 448.0
 MIN_SCALE = 1.0 / (FP8_MAX * 512.0)     # vLLM's minimum per-token scale (fp8_quant_fuse.py:78-79)
 
-_DT = {torch.bfloat16: _lib.H3FP8_DT_BF16, torch.float16: _lib.H3FP8_DT_FP16}
+_DT = {torch.bfloat16: _lib.H3FP8_DT_BF16, torch.float16: _lib.H3FP8_DT_FP16, torch.float32: _lib.H3FP8_DT_F32}
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -107,11 +107,12 @@ def gemm(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch
          out_dtype: torch.dtype = torch.bfloat16, bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
          row_amax: torch.Tensor | None = None) -> torch.Tensor:
     """y [M, N] = round(sa[m] * (sb[n] * (a @ w.T)[m, n])) (+ bias by one fma); ``w`` is the [N, K] weight.
-    With ``row_amax`` ([M] fp32) the epilogue also reduces max |y| per row (for the next layer's quant)."""
+    With ``row_amax`` ([M] fp32) the epilogue also reduces max |y| per row (for the next layer's quant).
+    ``out_dtype=torch.float32`` returns the raw fp32 accumulator (probe mode: scales ignored)."""
     N = w.shape[0]
     M, sa, sa_st, sb, sb_st = _gemm_args(a, w, scale_a, scale_b, N)
     if out_dtype not in _DT:
-        raise ValueError(f"out_dtype must be bf16 or fp16, got {out_dtype}")
+        raise ValueError(f"out_dtype must be bf16, fp16 or fp32 (probe), got {out_dtype}")
     if bias is not None and (bias.dim() != 1 or bias.numel() != N or bias.dtype != out_dtype):
         raise ValueError("bias must be [N] in the output dtype")
     y = out if out is not None else torch.empty((M, N), device=a.device, dtype=out_dtype)

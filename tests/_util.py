@@ -78,27 +78,75 @@ def bf16_from_bits(b: np.ndarray) -> np.ndarray:
     return (b.astype(np.uint32) << 16).view(np.float32)
 
 
-def check_close_bf16(y: torch.Tensor, ref_bits: np.ndarray, min_equal: float = 0.95, row_frac: float = 2.0 ** -10,
-                     ulps: float = 1.0):
-    """Tolerance for a bf16 GEMM output against the oracle (fp32-accumulated dequantised product, same epilogue).
+# Accumulation-error model of the gfx950 FP8 MFMA (v_mfma_f32_32x32x64_f8f6f4): each instruction sums its 64 products
+# with well under fp32 precision before adding them to the fp32 accumulator, and the error grows with the dynamic
+# range of the products.  Measured max |acc - exact| / sum_k |a_k w_k|: 2^-19.0 on serving-like operands (log-normal
+# rows), 2^-14.7 on N(0,1) activations with x40 outlier channels (K = 3072), 2^-15.8 (K = 8192); a sequential fp32 sum
+# stays below 2^-25.6.  The tolerances allow ACC_REL = 2^-12 (four times the worst seen); for N(0,1) activations that
+# is about 1 % of the output rms.  test_gemm_gpu.py::test_accumulator_error_model pins the bound on the raw fp32
+# accumulator.
+ACC_REL = 2.0 ** -12
 
-    The kernel and the oracle sum K in different orders, so their fp32 accumulators differ by a few fp32 ulps and a
-    bf16 rounding may flip.  Stated bound, per element:  |y - ref| <= ulp_bf16(ref) + 2^-10 * rms(row of ref)
-    (one bf16 ulp, plus an absolute slack for cancellation near zero), and at least ``min_equal`` of the outputs
-    bit-equal.  Returns (max |err| / rms, fraction bit-equal).  The whole-tensor form "max |err| <= 2e-2 * rms" is not
-    used: one ulp at |y| > 5 rms already exceeds it for bf16 outputs."""
+
+def abs_products(a: torch.Tensor, w: torch.Tensor) -> np.ndarray:
+    """sum_k |a[m,k]| |w[n,k]| in float64 (the scale of the accumulation error)."""
+    A = np.abs(O.e4m3_to_f32(bits8(a)).astype(np.float64))
+    W = np.abs(O.e4m3_to_f32(bits8(w)).astype(np.float64))
+    return A @ W.T
+
+
+def ulp_bf16(x: np.ndarray) -> np.ndarray:
+    mag = np.abs(x)
+    e = np.floor(np.log2(np.where(mag > 0, mag, 1.0)))
+    return np.where(mag > 0, np.exp2(e - 7), 2.0 ** -133)
+
+
+def check_close_bf16(y: torch.Tensor, ref_bits: np.ndarray, acc_err: np.ndarray, min_equal: float = 0.95):
+    """Tolerance for a bf16 GEMM output against the oracle (exact dequantised product, the same epilogue):
+    |y - ref| <= ulp_bf16(ref) + acc_err per element, acc_err = |sa sb| * ACC_REL * sum_k |a w| (the MFMA's
+    accumulation error carried through the scales), and at least ``min_equal`` of the outputs bit-equal.
+    Returns (max |err| / rms, fraction bit-equal).  The whole-tensor form "max |err| <= 2e-2 * rms" is not used: one
+    bf16 ulp at |y| > 5 rms already exceeds it."""
     out = f32(y).astype(np.float64)
     ref = bf16_from_bits(ref_bits).astype(np.float64)
     assert np.isfinite(out).all() and np.isfinite(ref).all()
-    mag = np.abs(ref)
-    e = np.floor(np.log2(np.where(mag > 0, mag, 1.0)))
-    ulp = np.where(mag > 0, np.exp2(e - 7), 0.0)
-    row_rms = np.sqrt(np.mean(ref * ref, axis=1, keepdims=True))
     err = np.abs(out - ref)
-    bound = ulps * ulp + row_frac * row_rms
+    bound = ulp_bf16(ref) + acc_err
     bad = err > bound
-    assert not bad.any(), f"{int(bad.sum())} outputs beyond {ulps} ulp + {row_frac} rms_row; worst {np.max(err - bound)}"
+    assert not bad.any(), f"{int(bad.sum())} outputs beyond 1 ulp + accumulation error; worst {np.max(err - bound)}"
     eq = float(np.mean(bits16(y) == ref_bits))
     assert eq >= min_equal, eq
     rms = float(np.sqrt(np.mean(ref * ref)))
     return float(err.max()) / rms, eq
+
+
+def gemm_acc_err(a, w, sa, sb) -> np.ndarray:
+    """Per-element bound of the accumulation error after the scales: |sa[m] sb[n]| ACC_REL sum_k |a w|."""
+    return np.abs(np.outer(f32(sa).reshape(-1).astype(np.float64), f32(sb).reshape(-1).astype(np.float64))) * \
+        ACC_REL * abs_products(a, w)
+
+
+def check_close_swiglu(h: torch.Tensor, acc_exact: np.ndarray, sa, sb, absum: np.ndarray, min_equal: float = 0.95):
+    """Tolerance for the fused gate/up GEMM + SwiGLU.  With the oracle's bf16 gate g, up u and silu s = silu_bf16(g)
+    from the exact product, each of g and u may move by one bf16 ulp plus its accumulation error (dg, du), s by up to
+    1.1 dg (|silu'| <= 1.1) plus one ulp (ds), and h by |u| ds + |s| du + ds du plus its own rounding."""
+    sa_n = f32(sa).reshape(-1).astype(np.float64)
+    sb_n = f32(sb).reshape(-1).astype(np.float64)
+    F = acc_exact.shape[1] // 2
+    g_bits = O.epilogue(acc_exact[:, :F].astype(np.float32), f32(sa).reshape(-1), f32(sb).reshape(-1)[:F])
+    u_bits = O.epilogue(acc_exact[:, F:].astype(np.float32), f32(sa).reshape(-1), f32(sb).reshape(-1)[F:])
+    g, u = bf16_from_bits(g_bits).astype(np.float64), bf16_from_bits(u_bits).astype(np.float64)
+    s = bf16_from_bits(O.silu_table()[g_bits]).astype(np.float64)
+    h_ref_bits = O.scale_swiglu(acc_exact.astype(np.float32), f32(sa), f32(sb))
+    href = bf16_from_bits(h_ref_bits).astype(np.float64)
+    dg = ulp_bf16(g) + np.abs(np.outer(sa_n, sb_n[:F])) * ACC_REL * absum[:, :F]
+    du = ulp_bf16(u) + np.abs(np.outer(sa_n, sb_n[F:])) * ACC_REL * absum[:, F:]
+    ds = 1.1 * dg + ulp_bf16(s)
+    bound = np.abs(u) * ds + np.abs(s) * du + ds * du + ulp_bf16(href)
+    out = f32(h).astype(np.float64)
+    err = np.abs(out - href)
+    bad = err > bound
+    assert not bad.any(), f"{int(bad.sum())} SwiGLU outputs beyond the propagated bound; worst {np.max(err - bound)}"
+    eq = float(np.mean(bits16(h) == h_ref_bits))
+    assert eq >= min_equal, eq
+    return eq
