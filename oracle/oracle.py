@@ -116,27 +116,33 @@ def _E4M3_LUT() -> np.ndarray:
 
 
 def e4m3fn_from_f32(x: np.ndarray) -> np.ndarray:
-    """Elementwise fp32 -> e4m3fn (RNE) through the C routine (the ``.to(float8_e4m3fn)`` of the reference)."""
-    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    """Elementwise (shape kept) fp32 -> e4m3fn (RNE) through the C routine (the ``.to(float8_e4m3fn)`` of the reference)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    shape = x.shape
+    x = x.ravel()
     out = np.empty(x.size, dtype=np.uint8)
     lib().oracle_e4m3fn_from_f32_array(_p(x), x.size, _p(out))
-    return out
+    return out.reshape(shape)
 
 
 def bf16_rne(x: np.ndarray) -> np.ndarray:
-    """Elementwise fp32 -> bf16 bits through the C routine (``_round_bf16`` / torch's cast)."""
-    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    """Elementwise (shape kept) fp32 -> bf16 bits through the C routine (``_round_bf16`` / torch's cast)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    shape = x.shape
+    x = x.ravel()
     out = np.empty(x.size, dtype=np.uint16)
     lib().oracle_bf16_rne_array(_p(x), x.size, _p(out))
-    return out
+    return out.reshape(shape)
 
 
 def fp16_rne(x: np.ndarray) -> np.ndarray:
-    """Elementwise fp32 -> fp16 bits through the C routine (torch's ``.to(torch.float16)``)."""
-    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    """Elementwise (shape kept) fp32 -> fp16 bits through the C routine (torch's ``.to(torch.float16)``)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    shape = x.shape
+    x = x.ravel()
     out = np.empty(x.size, dtype=np.uint16)
     lib().oracle_fp16_rne_array(_p(x), x.size, _p(out))
-    return out
+    return out.reshape(shape)
 
 
 def quant_rows(x_bf16_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:

@@ -1,0 +1,297 @@
+"""Pins of the CPU oracle (CPU only): every oracle function is checked against something it was not derived from --
+torch's and numpy's own casts and arithmetic, the golden fixtures of tests/golden/ (written by make_golden.py from
+torch's CPU routines in the reference mirrors' order), the known answers of the reference's tests, brute force on the
+e4m3 grid, exact rational / integer arithmetic, and invariants that a dropped term or a swapped operand breaks."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+E4M3 = torch.float8_e4m3fn
+
+
+def golden(name):
+    return np.load(os.path.join(GOLDEN, name))
+
+
+def f32_from_bits(u):
+    return np.asarray(u, dtype=np.uint32).view(np.float32)
+
+
+def sweep_patterns(n_random=1 << 21, seed=0):
+    """fp32 bit patterns: random, every special class, and the rounding boundaries of bf16/fp16/e4m3."""
+    rng = np.random.default_rng(seed)
+    r = rng.integers(0, 1 << 32, n_random, dtype=np.uint64).astype(np.uint32)
+    hi = rng.integers(0, 1 << 16, 4096, dtype=np.uint64).astype(np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    bnd = (hi[:, None] | lows[None, :]).reshape(-1)
+    spec = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0xFFC00000, 0x7F800001, 0x00000001,
+                     0x007FFFFF, 0x00800000, 0x7F7FFFFF, 0xFF7FFFFF], np.uint32)
+    return np.concatenate([r, bnd, spec])
+
+
+# ---- casts ----------------------------------------------------------------------------------------------------------
+
+def test_min_scale_constant():
+    assert np.float32(O.MIN_SCALE).view(np.uint32) == 0x36924925
+    assert O.lib().oracle_min_scale() == pytest.approx(4.359654212748865e-06, rel=1e-7)
+
+
+def test_bf16_rne_matches_torch_cast():
+    u = sweep_patterns()
+    x = f32_from_bits(u)
+    ours = O.bf16_rne(x)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(ours[~nan], ref[~nan])
+    assert np.all((ours[nan] & 0x7F80) == 0x7F80) and np.all(ours[nan] & 0x007F)
+
+
+def test_fp16_rne_matches_numpy_cast():
+    u = sweep_patterns(seed=1)
+    x = f32_from_bits(u)
+    ours = O.fp16_rne(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(ours[~nan], ref[~nan])
+    assert np.all(np.isnan(ours[nan].view(np.float16)))
+
+
+def test_e4m3_decode_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    ours = O.e4m3_to_f32(codes)
+    ref = torch.from_numpy(codes).view(E4M3).float().numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan) and nan.sum() == 2
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_e4m3_encode_matches_torch_cast_dense():
+    # every 37th fp32 pattern below 512 in magnitude (both signs) plus the general sweep
+    base = np.arange(0, 0x44000000, 37, dtype=np.uint32)
+    u = np.concatenate([base, base | 0x80000000, sweep_patterns(seed=2)])
+    x = f32_from_bits(u)
+    ours = O.e4m3fn_from_f32(x)
+    ref = torch.from_numpy(x.copy()).to(E4M3).view(torch.uint8).numpy()
+    nan = (ref & 0x7F) == 0x7F
+    assert np.array_equal((ours & 0x7F) == 0x7F, nan)
+    assert np.array_equal(ours[~nan], ref[~nan])
+
+
+def test_e4m3_encode_brute_force_nearest_even():
+    """Nearest grid value by exhaustive search over the 253 finite codes, ties to the even code."""
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.uniform(-448, 448, 20000), rng.uniform(-0.02, 0.02, 20000),
+                        rng.uniform(-1e-3, 1e-3, 5000)]).astype(np.float32)
+    grid_codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    grid = O.e4m3_to_f32(grid_codes).astype(np.float64)
+    d = np.abs(x.astype(np.float64)[:, None] - grid[None, :])
+    best = d.min(1, keepdims=True)
+    cand = d == best
+    # among tied candidates: the even mantissa code (lowest bit 0); +0 preferred for sign of zero by the value's sign
+    pick = np.empty(len(x), np.uint8)
+    for i in range(len(x)):
+        cs = grid_codes[cand[i]]
+        if len(cs) > 1:
+            cs = cs[(cs & 1) == 0] if np.any((cs & 1) == 0) else cs
+            if len(cs) > 1:                                  # +0 / -0: sign of x
+                cs = cs[(cs & 0x80) == (0x80 if np.signbit(x[i]) else 0)]
+        pick[i] = cs[0]
+    ours = O.e4m3fn_from_f32(x)
+    assert np.array_equal(ours, pick)
+
+
+def test_e4m3_grid_idempotent():
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    assert np.array_equal(O.e4m3fn_from_f32(O.e4m3_to_f32(codes)), codes)
+
+
+# ---- per-token quant ------------------------------------------------------------------------------------------------
+
+def test_quant_matches_golden():
+    gd = golden("quant.npz")
+    q, s = O.quant_rows(gd["x"])
+    assert np.array_equal(s.view(np.uint32), gd["scale"].view(np.uint32))
+    assert np.array_equal(q, gd["q"])
+    assert s[3] == O.MIN_SCALE and not q[3].any()               # the all-zero row
+
+
+def test_quant_every_bf16_row_maximum():
+    """Every positive finite bf16 as a row maximum: scale = max(amax / 448, MIN_SCALE) with IEEE division (numpy),
+    and the whole row against the golden sweep (torch's ops)."""
+    gd = golden("amax_sweep.npz")
+    q, s = O.quant_rows(gd["x"])
+    amax = (gd["x"][:, 0].astype(np.uint32) << 16).view(np.float32)
+    want = np.maximum(amax / np.float32(448.0), O.MIN_SCALE)
+    assert np.array_equal(s.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), gd["scale"].view(np.uint32))
+    assert np.array_equal(q, gd["q"])
+    big = amax / np.float32(448.0) >= O.MIN_SCALE
+    assert np.all(q[big, 0] == 0x7E) and np.all(q[big, 1] == 0xFE)   # the maximum lands on +-448
+
+
+def test_quant_uses_reciprocal_multiply():
+    """x * (1/scale), not x / scale: find rows where the two differ and check the oracle takes the reciprocal form."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((4000, 64)) * np.exp(rng.standard_normal((4000, 1)) * 2)).astype(np.float32)
+    xb = O.bf16_rne(x)
+    q, s = O.quant_rows(xb)
+    xf = O.bf16_to_f32(xb)
+    inv = np.float32(1.0) / s[:, None]
+    by_recip = O.e4m3fn_from_f32(np.clip(xf * inv, -448, 448))
+    by_div = O.e4m3fn_from_f32(np.clip(xf / s[:, None], -448, 448))
+    assert (by_recip != by_div).any()                         # the sample distinguishes the two forms
+    assert np.array_equal(q, by_recip)
+
+
+def test_quant_invariants():
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((500, 256)) * np.exp(rng.standard_normal((500, 1)) * 3)).astype(np.float32)
+    xb = O.bf16_rne(x)
+    q, s = O.quant_rows(xb)
+    qn, sn = O.quant_rows(xb ^ 0x8000)                       # negation flips the sign bit only
+    assert np.array_equal(sn, s)
+    nz = (q & 0x7F) != 0
+    assert np.array_equal(qn[nz], q[nz] ^ 0x80)
+    dec = O.e4m3_to_f32(q)
+    assert np.all(np.abs(dec) <= 448)
+    xf = O.bf16_to_f32(xb)
+    err = np.abs(dec * s[:, None] - xf)
+    assert np.all(err <= np.abs(xf) * 2.0 ** -4 + s[:, None] * 2.0 ** -10)   # half an e4m3 ulp (+ subnormal step)
+
+
+def test_quant_nonfinite_rows():
+    row_inf = np.zeros((1, 16), np.float32)
+    row_inf[0, :3] = [np.inf, 1.0, -1.0]
+    row_nan = np.ones((1, 16), np.float32)
+    row_nan[0, 5] = np.nan
+    q, s = O.quant_rows(O.bf16_rne(np.concatenate([row_inf, row_nan])))
+    assert np.isinf(s[0]) and (q[0, 0] & 0x7F) == 0x7F          # inf * (1/inf) = NaN
+    assert q[0, 1] == 0x00 and q[0, 2] == 0x80                   # finite * 0 = +-0
+    assert np.isnan(s[1]) and np.all((q[1] & 0x7F) == 0x7F)
+
+
+def test_quant_matches_torch_formula_random():
+    """The reference's quant_torch (fp8_quant_fuse.py:302-307) in torch ops on seeded bf16 rows."""
+    g = torch.Generator().manual_seed(7)
+    h = (torch.randn(300, 1000, generator=g) * torch.exp(torch.randn(300, 1, generator=g) * 3)).to(torch.bfloat16)
+    h[::37] = 0
+    amax = h.abs().max(dim=-1)[0].unsqueeze(-1).float()
+    scale = (amax / 448.0).clamp(min=O.MIN_SCALE.item())
+    ref = (h.float() * scale.reciprocal()).clamp(-448.0, 448.0).to(E4M3).view(torch.uint8).numpy()
+    q, s = O.quant_rows(h.view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(q, ref) and np.array_equal(s, scale.numpy().reshape(-1))
+
+
+# ---- epilogue -------------------------------------------------------------------------------------------------------
+
+def test_epilogue_matches_golden():
+    gd = golden("epilogue.npz")
+    assert np.array_equal(O.epilogue(gd["acc"], gd["sa"], gd["sb"]), gd["y_bf16"])
+    assert np.array_equal(O.epilogue(gd["acc"], gd["sa"], gd["sb"], out_fp16=True), gd["y_fp16"])
+    assert np.array_equal(O.epilogue(gd["acc"], gd["sa"], gd["sb"], gd["bias"]), gd["y_bias_bf16"])
+
+
+def test_epilogue_order_known_answer():
+    """tests/test_fp8_gemm.py:67-75 of the reference: (sb * x) * sa, which differs from (x * sa) * sb here."""
+    x = np.array([[1.0000001192092896]], np.float32)
+    sa, sb = np.array([3.0], np.float32), np.array([0.1], np.float32)
+    right = (sb[0] * x[0, 0]) * sa[0]
+    assert O.epilogue(x, sa, sb, out_fp16=True)[0, 0] == np.float16(right).view(np.uint16)
+    assert O.bf16_rne(np.full((1, 1), right, np.float32))[0, 0] == O.epilogue(x, sa, sb)[0, 0]
+    # cases where the order survives the final rounding: the oracle must give (sb * acc) * sa on every one
+    rng = np.random.default_rng(11)
+    n = 1 << 21
+    acc = rng.standard_normal(n).astype(np.float32) * 100
+    s_a = np.exp(rng.uniform(-9, -2, n)).astype(np.float32)
+    s_b = np.exp(rng.uniform(-9, -7, n)).astype(np.float32)
+    right = (s_b * acc) * s_a
+    naive = (acc * s_a) * s_b
+    for fp16 in (True, False):
+        cast = O.fp16_rne if fp16 else O.bf16_rne
+        idx = np.nonzero(cast(right) != cast(naive))[0]
+        assert len(idx) >= 5
+        for i in idx[:200]:
+            y = O.epilogue(acc[i:i + 1].reshape(1, 1), s_a[i:i + 1], s_b[i:i + 1], out_fp16=fp16)
+            assert y[0, 0] == cast(right[i:i + 1])[0]
+
+
+# ---- SiLU / SwiGLU --------------------------------------------------------------------------------------------------
+
+def test_silu_table_against_float64_and_torch_exp():
+    tab = O.silu_table()
+    g = O.bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)          # correctly rounded fp32 exp
+        s = g / (np.float32(1.0) + e)
+    ref = O.bf16_rne(s.astype(np.float32))
+    nan = np.isnan(g)
+    assert np.array_equal(tab[~nan], ref[~nan])
+    assert np.all((tab[nan] & 0x7F80) == 0x7F80)
+    # the reference's CPU mirror uses torch's fp32 exp, which is not correctly rounded in general; on the 65536 bf16
+    # gate values it gives the same silu after the bf16 rounding everywhere (NaN outputs compared as NaN)
+    torch_tab = golden("swiglu.npz")["silu_torch_exp"]
+    t_nan = ((torch_tab & 0x7F80) == 0x7F80) & ((torch_tab & 0x7F) != 0)
+    o_nan = ((tab & 0x7F80) == 0x7F80) & ((tab & 0x7F) != 0)
+    assert np.array_equal(t_nan, o_nan) and o_nan.sum() == 254 + 1      # 254 NaN gates and silu(-inf) = -inf / inf
+    assert np.array_equal(tab[~o_nan], torch_tab[~o_nan])
+
+
+def test_swiglu_matches_golden_directed():
+    gd = golden("swiglu.npz")
+    h = O.scale_swiglu(gd["x32"], gd["sa"], gd["sb"])
+    want = gd["h"]
+    nan = (want & 0x7F80) == 0x7F80
+    nan &= (want & 0x7F) != 0
+    assert np.array_equal((h & 0x7F80) == 0x7F80, (want & 0x7F80) == 0x7F80)
+    assert np.array_equal(h[~nan], want[~nan])
+
+
+def test_swiglu_negative_zero_up():
+    # gate 1 (silu > 0) with up = -0 -> +0; gate -1 (silu < 0) with up = +-0 -> -0
+    gu = O.bf16_rne(np.array([[1.0, -1.0, -0.0, -0.0], [1.0, -1.0, 0.0, 0.0]], np.float32))
+    h = O.swiglu_bf16(gu)
+    assert h.tolist() == [[0x0000, 0x8000], [0x0000, 0x8000]]
+
+
+def test_scale_swiglu_quant_is_composition():
+    rng = np.random.default_rng(8)
+    acc = (rng.standard_normal((40, 512)) * 50).astype(np.float32)
+    sa = np.exp(rng.uniform(-3, 0, 40)).astype(np.float32)
+    sb = np.exp(rng.uniform(-3, 0, 512)).astype(np.float32)
+    q, s = O.scale_swiglu_quant(acc, sa, sb)
+    q2, s2 = O.quant_rows(O.scale_swiglu(acc, sa, sb))
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    h = O.scale_swiglu(acc, sa, sb)
+    gu = O.epilogue(acc, sa, sb)
+    assert np.array_equal(h, O.swiglu_bf16(gu))
+
+
+# ---- product --------------------------------------------------------------------------------------------------------
+
+def test_dequant_matmul_exact_on_integers():
+    rng = np.random.default_rng(9)
+    a = rng.integers(-4, 5, (37, 256)).astype(np.float32)
+    w = rng.integers(-2, 3, (29, 256)).astype(np.float32)
+    ac, wc = O.e4m3fn_from_f32(a), O.e4m3fn_from_f32(w)
+    exact = (a.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+    assert np.array_equal(O.dequant_matmul(ac, wc), exact)
+    assert np.array_equal(O.matmul_f32(ac, wc), exact)
+
+
+def test_dequant_matmul_k_ascending_fp32():
+    rng = np.random.default_rng(10)
+    ac = rng.integers(0, 256, (8, 96)).astype(np.uint8)
+    wc = rng.integers(0, 256, (5, 96)).astype(np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    wc[(wc & 0x7F) == 0x7F] = 0
+    a, w = O.e4m3_to_f32(ac), O.e4m3_to_f32(wc)
+    ref = np.zeros((8, 5), np.float32)
+    for k in range(96):                                   # fp32, one rounding per multiply and per add, k ascending
+        ref = (ref + (a[:, k:k + 1] * w[None, :, k]).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(O.dequant_matmul(ac, wc), ref)
