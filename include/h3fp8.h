@@ -168,6 +168,9 @@ int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream);
  *   h3fp8_copy_silu_table  copies the current device's SiLU table (65536 uint16) to `out` (device memory).
  */
 int h3fp8_selfcheck_e4m3(uint64_t* mismatches, uint64_t* nan_bad);
+/*   h3fp8_selfcheck_bf16   the same sweep for the hardware fp32 -> bf16 pair conversion used by the GEMM epilogues,
+ *                          against the round-to-nearest-even rule of torch's cast (every fp32 pattern).  Synchronous. */
+int h3fp8_selfcheck_bf16(uint64_t* mismatches, uint64_t* nan_bad);
 int h3fp8_copy_silu_table(void* out, void* stream);
 
 #ifdef __cplusplus

@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "h3fp8_common.h"
@@ -10,14 +11,15 @@
 __device__ uint16_t g_h3_silu_table[65536];
 
 // Counters of the e4m3 conversion self-check.
-__device__ unsigned long long g_h3_cvt_counts[2];
+__device__ unsigned long long g_h3_cvt_counts[4];
 
 namespace {
 thread_local char t_err[512] = "";
 std::mutex g_init_mu;
 constexpr int kMaxDevices = 64;
-bool g_inited[kMaxDevices] = {};
+std::atomic<bool> g_inited[kMaxDevices] = {};
 const uint16_t* g_silu_ptr[kMaxDevices] = {};   // device address of each device's copy of g_h3_silu_table
+int g_cus[kMaxDevices] = {};                    // compute units of each device (persistent GEMM grid size)
 }  // namespace
 
 namespace h3host {
@@ -72,6 +74,21 @@ __global__ void __launch_bounds__(256) h3_selfcheck_e4m3_kernel() {
     if (nan_bad) atomicAdd(&g_h3_cvt_counts[1], nan_bad);
 }
 
+// The hardware pair conversion to bf16 against bf16_rne (the reference's rounding rule) on every fp32 pattern.
+__global__ void __launch_bounds__(256) h3_selfcheck_bf16_kernel() {
+    unsigned long long bad = 0, nan_bad = 0;
+    const uint64_t total = 1ull << 32;
+    const uint64_t step = (uint64_t)gridDim.x * 256u;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < total; i += step) {
+        float x = h3::u2f((uint32_t)i);
+        uint32_t hw = h3::cvt_bf16x2(x, 0.0f) & 0xffffu;
+        if (x != x) nan_bad += ((hw & 0x7f80u) != 0x7f80u) || !(hw & 0x7fu);
+        else bad += (hw != h3::bf16_rne(x));
+    }
+    if (bad) atomicAdd(&g_h3_cvt_counts[2], bad);
+    if (nan_bad) atomicAdd(&g_h3_cvt_counts[3], nan_bad);
+}
+
 __global__ void __launch_bounds__(256) h3_copy_table_kernel(uint16_t* out) {
     uint32_t i = blockIdx.x * 256u + threadIdx.x;
     out[i] = g_h3_silu_table[i];
@@ -86,8 +103,11 @@ int ensure_device_init() {
         set_error("device index %d out of range", dev);
         return H3FP8_EINVAL;
     }
+    if (g_inited[dev].load(std::memory_order_acquire)) return H3FP8_OK;
     std::lock_guard<std::mutex> lock(g_init_mu);
-    if (g_inited[dev]) return H3FP8_OK;
+    if (g_inited[dev].load(std::memory_order_relaxed)) return H3FP8_OK;
+    int cus = 0;
+    H3_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     hipStream_t s;
     H3_CHECK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     hipLaunchKernelGGL(h3_build_silu_table_kernel, dim3(65536 / 256), dim3(256), 0, s);
@@ -98,8 +118,15 @@ int ensure_device_init() {
     void* p = nullptr;
     H3_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_h3_silu_table)));
     g_silu_ptr[dev] = (const uint16_t*)p;
-    g_inited[dev] = true;
+    g_cus[dev] = cus > 0 ? cus : 1;
+    g_inited[dev].store(true, std::memory_order_release);
     return H3FP8_OK;
+}
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 1;
+    return g_cus[dev] > 0 ? g_cus[dev] : 1;
 }
 
 const uint16_t* silu_table_ptr() {
@@ -120,15 +147,29 @@ int h3fp8_init(void) { return h3host::ensure_device_init(); }
 
 int h3fp8_selfcheck_e4m3(uint64_t* mismatches, uint64_t* nan_bad) {
     H3_REQUIRE(mismatches && nan_bad, "h3fp8_selfcheck_e4m3: null output pointer");
-    unsigned long long zero[2] = {0, 0};
+    unsigned long long zero[4] = {0, 0, 0, 0};
     H3_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_h3_cvt_counts), zero, sizeof(zero)));
     hipLaunchKernelGGL(h3_selfcheck_e4m3_kernel, dim3(4096), dim3(256), 0, (hipStream_t)0);
     H3_CHECK_HIP(hipGetLastError());
     H3_CHECK_HIP(hipDeviceSynchronize());
-    unsigned long long out[2];
+    unsigned long long out[4];
     H3_CHECK_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(g_h3_cvt_counts), sizeof(out)));
     *mismatches = out[0];
     *nan_bad = out[1];
+    return H3FP8_OK;
+}
+
+int h3fp8_selfcheck_bf16(uint64_t* mismatches, uint64_t* nan_bad) {
+    H3_REQUIRE(mismatches && nan_bad, "h3fp8_selfcheck_bf16: null output pointer");
+    unsigned long long zero[4] = {0, 0, 0, 0};
+    H3_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_h3_cvt_counts), zero, sizeof(zero)));
+    hipLaunchKernelGGL(h3_selfcheck_bf16_kernel, dim3(4096), dim3(256), 0, (hipStream_t)0);
+    H3_CHECK_HIP(hipGetLastError());
+    H3_CHECK_HIP(hipDeviceSynchronize());
+    unsigned long long out[4];
+    H3_CHECK_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(g_h3_cvt_counts), sizeof(out)));
+    *mismatches = out[2];
+    *nan_bad = out[3];
     return H3FP8_OK;
 }
 

@@ -5,25 +5,31 @@
 //   y[m, n] = round(sa[m] * (sb[n] * acc[m, n])), acc = sum_k a[m, k] * w[n, k] in fp32, K ascending per
 //   accumulator, no split-K; with a bias: round(fma(sa[m], sb[n] * acc, bias[n])).
 //
-// Tiling (one workgroup = 4 wavefronts = 256 threads, one workgroup per CU):
+// Tiling (one workgroup = 4 wavefronts = 256 threads, one persistent workgroup per CU):
 //   * block tile 256 (tokens m) x 256 (channels n) x 128 (k); each wave owns a 128 x 128 sub-tile: 4 x 4 MFMA tiles of
 //     v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3 -> fp32), two k sub-steps per stage, 256 fp32 accumulators per lane (the
 //     AGPR file);
 //   * the MFMA's A operand is the weight tile (rows n) and its B operand the activation tile (rows m), so each group of
-//     four accumulators of a lane holds four consecutive channels n of one token m: the epilogue stores 8 bytes;
+//     four accumulators of a lane holds four consecutive channels n of one token m;
 //   * global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging): each instruction moves 8 rows x 128 bytes, i.e.
 //     whole 128-byte lines (64-byte row pieces halve the load path's throughput: measured 22 vs 40 bytes/clk/CU);
 //     out-of-range rows and the K tail read as zero through the buffer descriptor's range check;
 //   * two LDS stages (2 x 64 KiB); a stage is released by a barrier right after the last reads of its k-step (early in
-//     the step), so the loads of k-step i+2 run during about 44 MFMAs (about 1.5 k-steps);
+//     the step), and the loads of k-step i+2 are issued one per MFMA over the following 16 MFMAs (issued in bursts they
+//     stall the instruction stream);
+//   * persistent tile loop: the load cursor runs two k-steps ahead of the MFMAs across tile boundaries, so the next
+//     tile's first stages and its scales (DMA'd into one of three LDS scale sets) load while the current tile's last
+//     k-steps and its epilogue run; the epilogue stages its output in a separate 4 KiB area per wave;
 //   * LDS rows are 128 bytes; 16-byte chunk c of row r is stored at chunk c ^ swz(r), swz(r) = ((r >> 1) & 7) ^
 //     ((r & 1) << 2): eight consecutive rows (32 banks) and sixteen (64 banks) read at one logical chunk never share a
 //     bank (conflict-free ds_read_b128);
 //   * operand fragments are double-buffered in VGPRs: sub-step 1 is read while sub-step 0 multiplies, and the next
-//     stage's sub-step 0 right after the barrier that publishes it, while the last MFMAs of the step run;
+//     stage's sub-step 0 right after the barrier that publishes it, in the order the first MFMAs consume them;
 //   * stage release: a stage is refilled only after a barrier that every wave reaches with lgkmcnt(0), i.e. after all
 //     of its ds_reads have returned;
-//   * tile order: workgroups are spread over the 8 XCDs round-robin by the hardware, so the block index is remapped to
+//   * every k-step runs the same branch-free instruction stream (no k-step g+2: out-of-range loads; no tile start:
+//     the scale loads go to a scratch slot), so the MFMA stream is never broken by a branch;
+//   * tile order: workgroups are spread over the 8 XCDs round-robin by the hardware, so the tile index is remapped to
 //     give every XCD a contiguous range of tiles, walked in groups of GROUP_M row tiles (L2 reuse of both operands).
 // SwiGLU variant: the weight tile is 128 gate rows f0.. and the 128 matching up rows F+f0..; each wave holds the gate
 // and up accumulators of the same (m, f) and applies fp8_swiglu.py:64-70 in registers.
@@ -44,7 +50,7 @@ constexpr int ROWB = BK;         // bytes per LDS row
 constexpr int STAGE_BYTES = (BM + BN) * ROWB;   // 64 KiB
 constexpr int NSTAGE = 2;
 constexpr int A_REGION = BN * ROWB;             // activation rows start after the weight rows
-constexpr int MFMA_SPLIT = 12;                  // sub-step-1 MFMAs issued before the stage barrier (of 16)
+constexpr int MFMA_SPLIT = 10;                  // sub-step-1 MFMAs issued before the stage barrier (of 16)
 constexpr uint32_t OOB = 0x80000000u;         // an offset past every buffer's range: the load returns zeros
 
 enum Epi { EPI_PLAIN = 0, EPI_AMAX = 1, EPI_SWIGLU = 2 };
@@ -61,6 +67,7 @@ struct GemmParams {
     int64_t lda, ldw, ldy;
     int64_t sa_stride, sb_stride;
     int M, N, K;               // SwiGLU: N = F (output width)
+    int w_rows;                // rows of w and entries of sb (N, or 2F for SwiGLU)
     uint32_t a_bytes, w_bytes; // buffer ranges
     int tiles_m, tiles_n;
     int group_m;
@@ -145,12 +152,36 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8)(p));
 }
 
-// Per-wave state of the mainloop.
+// 4 bytes per lane straight into LDS at lds_base + 4 * lane (buffer_load_dword ... lds); untracked like dma16.
+__device__ __forceinline__ void dma4(v4u desc, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(desc)
+                 : "memory", "m0");
+}
+
+// ---- LDS layout of a workgroup (150 KiB of the 160 KiB) ----
+//   [0, 128 KiB)          two operand stages of 64 KiB (weight rows, then token rows, 128 bytes each)
+//   [128 KiB, 144 KiB)    epilogue staging, 4 KiB per wave: 32 token rows x 64 channels of bf16
+//   [144 KiB, 150 KiB)    three scale sets of 2 KiB: sa of the tile's 256 token rows, then sb of its 256 weight rows
+//   [150 KiB, +512)       a scratch slot for the scale loads of k-steps that do not start a tile
+// The stages are never used by the epilogue, so the loads of the next tile run under it.
+constexpr int STAGING_PER_WAVE = 32 * 128;
+constexpr int STAGING_OFF = NSTAGE * STAGE_BYTES;
+constexpr int SCALE_SET = 2 * 256 * 4;
+constexpr int NSCALE = 3;
+constexpr int SCALES_OFF = STAGING_OFF + 4 * STAGING_PER_WAVE;
+constexpr int JUNK_OFF = SCALES_OFF + NSCALE * SCALE_SET;   // 512 bytes: target of the scale loads that are not needed
+constexpr int LDS_TOTAL = JUNK_OFF + 512;
+
+// Per-wave addressing of one tile's global -> LDS loads.
 struct Loader {
-    v4u rw, ra;
+    v4u rw, ra;                 // weight / activation buffer descriptors
+    v4u rsa, rsb;               // scale buffer descriptors
     uint32_t vw[2], va[2];      // lane part of the byte offsets for even / odd instructions (OOB: share out of range)
     uint32_t c16[2];            // 16 * logical chunk of this lane for even / odd instructions
     uint32_t row8_w, row8_a;    // byte advance of 8 rows
+    uint32_t sa_off, sb_off;    // this lane's scale offsets (OOB past the range)
     int K;
     int w_groups;               // SwiGLU: 8-row groups of this wave's weight share that are in range
 };
@@ -162,22 +193,6 @@ struct StageIssue {
 };
 
 template <int EPI>
-__device__ __forceinline__ StageIssue stage_issue(uint8_t* stage, const Loader& L, int wave, int ks) {
-    StageIssue S;
-    const uint32_t k0 = (uint32_t)ks * BK;
-    const bool tail = (int)k0 + BK > L.K;                      // K tail: chunks at or past K read zeros
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const bool dead = tail && (k0 + L.c16[e]) >= (uint32_t)L.K;
-        S.vw[e] = dead ? OOB : L.vw[e] + k0;
-        S.va[e] = dead ? OOB : L.va[e] + k0;
-    }
-    S.wdst = lds_addr(stage + wave * 64 * ROWB);
-    S.adst = lds_addr(stage + A_REGION + wave * 64 * ROWB);
-    return S;
-}
-
-template <int EPI>
 __device__ __forceinline__ void issue_one(const StageIssue& S, const Loader& L, int i) {
     if (i < 8) {
         const uint32_t off = (EPI == EPI_SWIGLU && i >= L.w_groups) ? OOB : S.vw[i & 1] + i * L.row8_w;
@@ -185,13 +200,6 @@ __device__ __forceinline__ void issue_one(const StageIssue& S, const Loader& L, 
     } else {
         dma16(L.ra, S.adst + (i - 8) * 8 * ROWB, S.va[i & 1] + (i - 8) * L.row8_a);
     }
-}
-
-template <int EPI>
-__device__ __forceinline__ void issue_stage(uint8_t* stage, const Loader& L, int wave, int ks) {
-    const StageIssue S = stage_issue<EPI>(stage, L, wave, ks);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) issue_one<EPI>(S, L, i);
 }
 
 // Weight-tile row of MFMA tile tn (0..3) of wave column wn.
@@ -223,93 +231,50 @@ __device__ __forceinline__ void mfma_one(v16f acc[4][4], const v8i af[4], const 
                                                                          0, 0, 0, 0);
 }
 
-// MFMAs number lo .. hi-1 of the 16 of one sub-step (tile (i, j) = MFMA 4 i + j).
-__device__ __forceinline__ void mfma_range(v16f acc[4][4], const v8i af[4], const v8i bf[4], int lo, int hi) {
+struct GroupedParams {
+    GemmParams g[H3FP8_MAX_GROUPS];
+    int n;
+    int total_tiles;           // tiles of all problems (problem i owns [g[i].tile_offset, + tiles_m * tiles_n))
+};
+
+template <bool GROUPED>
+__device__ __forceinline__ int problem_of(const GroupedParams& gp, int id) {
+    int i = 0;
+    if (GROUPED) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t)
-        if (t >= lo && t < hi)
-            acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[t >> 2], bf[t & 3], acc[t >> 2][t & 3],
-                                                                                 0, 0, 0, 0, 0, 0);
+        for (int j = 1; j < H3FP8_MAX_GROUPS; ++j)
+            if (j < gp.n && id >= gp.g[j].tile_offset) i = j;
+    }
+    return i;
 }
 
-// One k-step.  On entry stage ks & 1 holds k-step ks, its sub-step-0 fragments are in f0, and the loads of k-step
-// ks+1 into the other stage are in flight.
-//   phase A: the 16 sub-step-0 MFMAs, with the reads of the 8 sub-step-1 fragments issued between the first 8;
-//   barrier 1 (after lgkmcnt(0)): every wave's reads of this stage have returned -- the stage is free;
-//   phase B: the 16 sub-step-1 MFMAs, with the 16 load instructions of k-step ks+2 into the freed stage issued two per
-//   MFMA between the first 8 (loads and reads are spread between MFMAs so that a stalled issue of a memory instruction
-//   never holds the matrix core idle), then, once this wave's share of k-step ks+1 has landed (vmcnt(16)), barrier 2
-//   publishes it and the sub-step-0 fragments of ks+1 are read between the last MFMA_SPLIT..15 MFMAs.
-// The loads of k-step ks+2 therefore have about 1.5 k-steps (about 40 MFMAs) to land.
+// Global tile id -> problem and tile coordinates.
+template <bool GROUPED>
+__device__ __forceinline__ int locate(const GroupedParams& gp, int id, int& tm, int& tn) {
+    const int pi = problem_of<GROUPED>(gp, id);
+    const GemmParams& p = gp.g[pi];
+    tile_of(id - p.tile_offset, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    return pi;
+}
+
+// Addressing of tile (tm, tn) of problem p for this wave.
+// lane l of an instruction covers row (l >> 3) of an 8-row group and LDS chunk (l & 7), i.e. logical chunk
+// (l & 7) ^ swz(row); swz depends on the row's bits 0..3, so even and odd groups of 8 rows differ.
 template <int EPI>
-__device__ __forceinline__ void kstep(uint8_t* lds, const Loader& L, int wave, int wn, int wm, int lane, int ks, int nk,
-                                      v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4], v8i fb1[4]) {
-    uint8_t* cur = lds + (ks & 1) * STAGE_BYTES;
-    uint8_t* nxt = lds + ((ks + 1) & 1) * STAGE_BYTES;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        mfma_one(acc, fa0, fb0, t);
-        if (t < 8) read_one<EPI>(cur, wn, wm, lane, 1, t, fa1, fb1);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    wait_lgkm0();                                       // this wave's reads of stage ks & 1 have returned
-    barrier_nofence();                                  // ... and every wave's: the stage is free
-    const bool load2 = ks + 2 < nk;
-    const StageIssue S = stage_issue<EPI>(cur, L, wave, ks + 2);
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        mfma_one(acc, fa1, fb1, t);
-        if (t < 8 && load2) {
-            issue_one<EPI>(S, L, 2 * t);
-            issue_one<EPI>(S, L, 2 * t + 1);
-        }
-        if (t == MFMA_SPLIT - 1 && ks + 1 < nk) {
-            if (load2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));     // k-step ks+1 landed (ks+2 may be in flight)
-            else wait_vm0();
-            barrier_nofence();
-        }
-        if (t >= MFMA_SPLIT && ks + 1 < nk) {
-            // spread the 8 fragment reads of k-step ks+1 over the MFMAs after barrier 2
-            constexpr int PER = (8 + (16 - MFMA_SPLIT) - 1) / (16 - MFMA_SPLIT);
-#pragma unroll
-            for (int f = (t - MFMA_SPLIT) * PER; f < (t - MFMA_SPLIT + 1) * PER; ++f)
-                if (f < 8) read_one<EPI>(nxt, wn, wm, lane, 0, f, fa0, fb0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-template <int OUT_DT, bool HAS_BIAS, int EPI>
-__device__ __forceinline__ void gemm_body(const GemmParams& p, int bid) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE_BYTES];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wn = wave & 1, wm = wave >> 1;
-
-    int tile_m, tile_n;
-    tile_of(bid, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
-    const int m0 = tile_m * BM;
-
-    // ---- global -> LDS addressing ----
-    // lane l of an instruction covers row (l >> 3) of an 8-row group and LDS chunk (l & 7), i.e. logical chunk
-    // (l & 7) ^ swz(row); swz depends on the row's bits 0..3, so even and odd groups of 8 rows differ.
-    Loader L;
+__device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn, int wave, int lane, Loader& L) {
     const uint32_t lrow = (uint32_t)(lane >> 3);
-    // LDS chunk of the lane is lane & 7; its row is 8 i + lrow of the share (even i: row & 8 == 0, odd i: 8)
     const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz((int)lrow)), (uint32_t)((lane & 7) ^ swz((int)lrow + 8))};
     int64_t wrow0;   // first global weight row of this wave's 64-row share
     int64_t wlimit;  // rows of this share's source range (SwiGLU gate rows stop at F)
     if (EPI == EPI_SWIGLU) {
-        const int f0 = tile_n * (BN / 2);
+        const int f0 = tn * (BN / 2);
         wrow0 = (wave < 2) ? (int64_t)f0 + 64 * wave : (int64_t)p.N + f0 + 64 * (wave - 2);
         wlimit = (wave < 2) ? (int64_t)p.N : 2 * (int64_t)p.N;
     } else {
-        wrow0 = (int64_t)tile_n * BN + 64 * wave;
+        wrow0 = (int64_t)tn * BN + 64 * wave;
         wlimit = p.N;
     }
-    const int64_t arow0 = (int64_t)m0 + 64 * wave;
+    const int64_t arow0 = (int64_t)tm * BM + 64 * wave;
     L.rw = buffer_desc(p.w, p.w_bytes);
     L.ra = buffer_desc(p.a, p.a_bytes);
 #pragma unroll
@@ -324,35 +289,165 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int bid) {
     // Partial shares rely on the descriptor's range check (rows >= M or >= N start past the last valid byte), except
     // SwiGLU gate rows past F, which would read up rows: those 8-row groups are zero-filled (F % 16 == 0).
     L.w_groups = (int)min<int64_t>(8, max<int64_t>(0, (wlimit - wrow0 + 7) / 8));
+    // scales: token row 64 wave + lane of the tile; weight row 64 wave + lane (SwiGLU: gate rows for waves 0-1, the
+    // matching up rows for waves 2-3)
+    L.rsa = buffer_desc(p.sa, p.sa_stride ? (uint32_t)((p.M - 1) * p.sa_stride * 4 + 4) : 4u);
+    L.rsb = buffer_desc(p.sb, p.sb_stride ? (uint32_t)((p.w_rows - 1) * p.sb_stride * 4 + 4) : 4u);
+    const int64_t srow = arow0 + lane;
+    L.sa_off = (srow < p.M) ? (uint32_t)(srow * p.sa_stride * 4) : OOB;
+    const int64_t wr = wrow0 + lane;
+    L.sb_off = (wr < wlimit) ? (uint32_t)(wr * p.sb_stride * 4) : OOB;
+}
 
-    const int nk = (p.K + BK - 1) / BK;             // k-steps of 128
+// The load-issue cursor: the (tile, k-step) whose operands are loaded next, two k-steps ahead of the MFMAs.
+struct Cursor {
+    Loader L;
+    int c;          // workgroup-local tile ordinal (global tile id = blockIdx.x + c * gridDim.x)
+    int ks, nk;
+    bool valid;
+};
 
-    v16f acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+template <int EPI, bool GROUPED>
+__device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, int c, int wave, int lane) {
+    const int id = (int)blockIdx.x + c * (int)gridDim.x;
+    I.c = c;
+    I.ks = 0;
+    I.valid = id < gp.total_tiles;
+    if (!I.valid) return;
+    int tm, tn;
+    const int pi = locate<GROUPED>(gp, id, tm, tn);
+    const GemmParams& p = gp.g[pi];
+    I.nk = (p.K + BK - 1) / BK;
+    make_loader<EPI>(p, tm, tn, wave, lane, I.L);
+}
 
-    // prologue: k-steps 0 and 1 in flight, the sub-step-0 fragments of k-step 0 in registers
-    v8i fa0[4], fb0[4], fa1[4], fb1[4];
-    issue_stage<EPI>(lds, L, wave, 0);
-    if (nk > 1) {
-        issue_stage<EPI>(lds + STAGE_BYTES, L, wave, 1);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));
-    } else {
-        wait_vm0();
+// The load instructions of the cursor's k-step for this wave.  Past the last tile every offset is out of range: the
+// loads still run (so that every k-step has the same instruction stream and wait counts) and fill the stage with zeros.
+template <int EPI>
+__device__ __forceinline__ StageIssue stage_issue(uint32_t stage, const Cursor& I, int wave) {
+    const Loader& L = I.L;
+    StageIssue S;
+    const uint32_t k0 = (uint32_t)I.ks * BK;
+    const bool tail = (int)k0 + BK > L.K;                      // K tail: chunks at or past K read zeros
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const bool dead = !I.valid || (tail && (k0 + L.c16[e]) >= (uint32_t)L.K);
+        S.vw[e] = dead ? OOB : L.vw[e] + k0;
+        S.va[e] = dead ? OOB : L.va[e] + k0;
     }
-    barrier_nofence();
-    read_frags<EPI>(lds, wn, wm, lane, 0, fa0, fb0);
-    for (int ks = 0; ks < nk; ++ks) kstep<EPI>(lds, L, wave, wn, wm, lane, ks, nk, acc, fa0, fb0, fa1, fb1);
+    S.wdst = __builtin_amdgcn_readfirstlane(stage + wave * 64 * ROWB);       // wave-uniform: an SGPR for m0
+    S.adst = __builtin_amdgcn_readfirstlane(stage + A_REGION + wave * 64 * ROWB);
+    return S;
+}
 
-    // ---- epilogue ----
-    // The scaled, rounded outputs go through LDS so that global stores are whole 16-byte pieces of contiguous row
-    // segments (a wave's 128 x 128 tile leaves the MFMA layout with only 8 contiguous bytes per lane and row).
-    // 32x32 MFMA result: lane l, register 4q + r holds D[8q + 4(l >> 5) + r][l & 31], i.e. channel
-    // n = tile_n_base + 8q + 4(l >> 5) + r of token m = tile_m_base + (l & 31).
+template <int EPI>
+__device__ __forceinline__ void issue_stage(uint32_t stage, const Cursor& I, int wave) {
+    const StageIssue S = stage_issue<EPI>(stage, I, wave);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) issue_one<EPI>(S, I.L, i);
+}
+
+// The scales of the cursor's tile when its k-step starts the tile: wave w loads sa of token rows 64 w .. 64 w + 63
+// and sb of weight rows 64 w .. 64 w + 63 into scale set c % NSCALE (a scalar scale has stride 0 and fills every
+// entry).  At any other k-step the two loads read nothing and land in the scratch slot.
+__device__ __forceinline__ void issue_scales(uint32_t lds0, const Cursor& I, int wave) {
+    const bool real = I.valid && I.ks == 0;
+    const uint32_t base = lds0 + SCALES_OFF + (uint32_t)(I.c % NSCALE) * SCALE_SET;
+    const uint32_t dsa = __builtin_amdgcn_readfirstlane(real ? base + 256 * wave : lds0 + JUNK_OFF);
+    const uint32_t dsb = __builtin_amdgcn_readfirstlane(real ? base + 1024 + 256 * wave : lds0 + JUNK_OFF + 256);
+    dma4(I.L.rsa, dsa, real ? I.L.sa_off : OOB);
+    dma4(I.L.rsb, dsb, real ? I.L.sb_off : OOB);
+}
+
+template <int EPI, bool GROUPED>
+__device__ __forceinline__ void cursor_next(Cursor& I, const GroupedParams& gp, int wave, int lane) {
+    if (++I.ks == I.nk) cursor_set<EPI, GROUPED>(I, gp, I.c + 1, wave, lane);
+}
+
+// One k-step g (stage g & 1 holds it, its sub-step-0 fragments are in fa0/fb0, the loads of k-step g+1 are in flight;
+// the cursor points at k-step g+2, possibly of the next tile).  The instruction stream is the same for every k-step:
+// when there is no k-step g+2 the 16 loads are issued with out-of-range offsets (they fill the freed stage with zeros
+// and touch no memory), the two scale loads go to a scratch slot of the LDS unless g+2 starts a tile, and after the
+// last k-step the extra fragment reads of the other stage are simply not used.
+//   phase A: the 16 sub-step-0 MFMAs, with the reads of the 8 sub-step-1 fragments issued between the first 8;
+//   barrier 1 (after lgkmcnt(0)): every wave's reads of this stage have returned -- the stage is free;
+//   phase B: the 16 sub-step-1 MFMAs, with the 16 load instructions of k-step g+2 into the freed stage issued one per
+//   MFMA (DMA_SPREAD) or two per MFMA over the first 8, then the two scale loads; once this wave's share of k-step g+1
+//   has landed (vmcnt: only the instructions issued in this phase may be outstanding), barrier 2 publishes it and the
+//   sub-step-0 fragments of g+1 are read between the last 16 - MFMA_SPLIT MFMAs.
+constexpr bool DMA_SPREAD = true;
+// order of the next k-step's sub-step-0 fragment reads (0..3 weight tiles, 4..7 token tiles): MFMA t of phase A uses
+// weight tile t / 4 and token tile t % 4, so reading weight tile 0 and then the token tiles lets it start earliest
+constexpr int NEXT_READ_ORDER[8] = {0, 4, 5, 6, 7, 1, 2, 3};
+
+template <int EPI>
+__device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, int wave, int wn, int wm,
+                                      int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4], v8i fb1[4]) {
+    uint8_t* cur = lds + (g & 1) * STAGE_BYTES;
+    uint8_t* nxt = lds + ((g + 1) & 1) * STAGE_BYTES;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        mfma_one(acc, fa0, fb0, t);
+        if (t < 8) read_one<EPI>(cur, wn, wm, lane, 1, t, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_lgkm0();                                       // this wave's reads of stage g & 1 have returned
+    barrier_nofence();                                  // ... and every wave's: the stage is free
+    const StageIssue S = stage_issue<EPI>(lds0 + (uint32_t)(g & 1) * STAGE_BYTES, I, wave);
+    // load instructions issued before the vmcnt wait of MFMA MFMA_SPLIT - 1
+    constexpr int BEFORE = (DMA_SPREAD ? MFMA_SPLIT : 16) + 2;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        mfma_one(acc, fa1, fb1, t);
+        if (DMA_SPREAD) {
+            issue_one<EPI>(S, I.L, t);
+        } else if (t < 8) {
+            issue_one<EPI>(S, I.L, 2 * t);
+            issue_one<EPI>(S, I.L, 2 * t + 1);
+        }
+        if (t == 8) issue_scales(lds0, I, wave);
+        if (t == MFMA_SPLIT - 1) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(BEFORE));   // k-step g+1 (and everything older) has landed
+            barrier_nofence();
+        }
+        if (t >= MFMA_SPLIT) {
+            // spread the 8 fragment reads of k-step g+1 over the MFMAs after barrier 2
+            constexpr int PER = (8 + (16 - MFMA_SPLIT) - 1) / (16 - MFMA_SPLIT);
+#pragma unroll
+            for (int f = (t - MFMA_SPLIT) * PER; f < (t - MFMA_SPLIT + 1) * PER; ++f)
+                if (f < 8) read_one<EPI>(nxt, wn, wm, lane, 0, NEXT_READ_ORDER[f], fa0, fb0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// max(m, |lo half|, |hi half|) of a packed bf16 pair, as fp32 bit patterns (the row maximum of the fused quant).
+__device__ __forceinline__ uint32_t max_abs_bf16x2(uint32_t m, uint32_t p) {
+    const uint32_t lo = (p << 16) & 0x7fff0000u, hi = p & 0x7fff0000u;
+    m = m > lo ? m : lo;
+    return m > hi ? m : hi;
+}
+
+// x + 0: -0 becomes +0 (round to nearest), every other value (NaN included) is unchanged.
+__device__ __forceinline__ float zero_to_pos(float x) {
+    float z = 0.0f;
+    asm volatile("" : "+v"(z));                         // an opaque zero: the add is not folded away
+    return x + z;
+}
+
+// ---- epilogue ----
+// 32x32 MFMA result: lane l, register 4q + r holds D[8q + 4(l >> 5) + r][l & 31], i.e. weight row (channel)
+// 8q + 4(l >> 5) + r of the MFMA tile and token l & 31.  The scaled, rounded outputs go through the wave's staging
+// area, 32 tokens x 64 channels at a time, so that global stores are 16-byte pieces of 128-byte row segments.
+// Scales come from the tile's scale set in LDS (loaded with the tile's first k-step).
+template <int OUT_DT, bool HAS_BIAS, int EPI>
+__device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, uint8_t* lds, int set, int wave, int wn,
+                                         int wm, int lane, v16f acc[4][4]) {
+    const int hi = lane >> 5;
+    const int mj = lane & 31;
+    const int mrow0 = tm * BM + wm * 128;               // first token row of the wave
+    const float* sa_l = reinterpret_cast<const float*>(lds + SCALES_OFF + set * SCALE_SET);
+    const float* sb_l = sa_l + 256;
     if (OUT_DT == H3FP8_DT_F32) {
         // probe mode: the raw fp32 accumulators, scales / bias / rounding not applied (16-byte stores per lane)
         float* yf = reinterpret_cast<float*>(p.y);
@@ -362,8 +457,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int bid) {
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int n = tile_n * BN + wn * 128 + 32 * i + 8 * q + 4 * (lane >> 5);
-                    const int m = m0 + wm * 128 + 32 * j + (lane & 31);
+                    const int n = tn * BN + wn * 128 + 32 * i + 8 * q + 4 * hi;
+                    const int m = mrow0 + 32 * j + mj;
                     if (n < p.N && m < p.M) {
                         const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                                        acc[i][j][4 * q + 3]};
@@ -372,146 +467,178 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int bid) {
                 }
         return;
     }
-    wait_lgkm0();
-    barrier_nofence();                                  // every wave is done with the stages: reuse the LDS
-    constexpr int OUT_COLS = (EPI == EPI_SWIGLU) ? 64 : 128;   // output columns per wave
-    constexpr int ROW_BYTES = OUT_COLS * 2;
-    constexpr int CHUNKS = ROW_BYTES / 16;                       // 16-byte chunks per row: 16 or 8
-    uint8_t* tile = lds + wave * (128 * ROW_BYTES);
-    // element (ml, cl) of the wave tile: row ml, 16-byte chunk (cl / 8) ^ (ml % CHUNKS), 8-byte half (cl / 4) % 2
-    auto put4 = [&](int ml, int cl, uint32_t lo, uint32_t hi2) {
-        const int ch = (cl >> 3) ^ (ml & (CHUNKS - 1));
-        *reinterpret_cast<uint2*>(tile + ml * ROW_BYTES + ch * 16 + ((cl >> 2) & 1) * 8) = make_uint2(lo, hi2);
+    uint8_t* stg = lds + STAGING_OFF + wave * STAGING_PER_WAVE;
+    // element (ml, cl) of the 32 x 64 staging tile: row ml, 16-byte chunk (cl / 8) ^ (ml % 8), 8-byte half (cl / 4) % 2
+    auto put4 = [&](int ml, int cl, uint32_t lo, uint32_t h2) {
+        const int ch = (cl >> 3) ^ (ml & 7);
+        *reinterpret_cast<uint2*>(stg + ml * 128 + ch * 16 + ((cl >> 2) & 1) * 8) = make_uint2(lo, h2);
     };
-    const int hi = lane >> 5;
-    const int mj = lane & 31;
-    const int mrow0 = m0 + wm * 128;
-    uint32_t rmax[4] = {0, 0, 0, 0};
-    float sam[4];
+    // the wave reads back its own staging tile (LDS accesses of one wave complete in order): 16 bytes per lane, 8
+    // lanes per 128-byte row segment, 8 rows per store instruction
+    uint16_t* ybase = reinterpret_cast<uint16_t*>(p.y);
+    auto flush = [&](int m0, int col0, int ncols) {
+        const int c = lane & 7;
+        const int col = col0 + c * 8;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = mrow0 + 32 * j + mj;
-        sam[j] = (m < p.M) ? p.sa[(int64_t)m * p.sa_stride] : 0.0f;
-    }
-    int col0, ncols;                                    // first output column of the wave, output width
+        for (int it = 0; it < 4; ++it) {
+            const int ml = it * 8 + (lane >> 3);
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+            const int m = m0 + ml;
+            if (m < p.M && col < ncols) *reinterpret_cast<uint4*>(ybase + (int64_t)m * p.ldy + col) = v;
+        }
+    };
+    auto row_amax = [&](uint32_t v, int m) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, 32, 64);
+        v = v > o ? v : o;
+        if (hi == 0 && m < p.M && v) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, v);
+    };
     if (EPI == EPI_SWIGLU) {
         const int F = p.N;
-        col0 = tile_n * (BN / 2) + wn * 64;
-        ncols = F;
+        const int col0 = tn * (BN / 2) + wn * 64;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int j = 0; j < 4; ++j) {
+            const int m = mrow0 + 32 * j + mj;
+            const float sam = sa_l[wm * 128 + 32 * j + mj];
+            uint32_t rmax = 0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int cl = 32 * t + 8 * q + 4 * hi;
-                const int f = col0 + cl;
-                const bool fok = f < F;
-                float sbg[4], sbu[4], bg[4] = {0, 0, 0, 0}, bu[4] = {0, 0, 0, 0};
+            for (int t = 0; t < 2; ++t) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    sbg[r] = fok ? p.sb[(int64_t)(f + r) * p.sb_stride] : 0.0f;
-                    sbu[r] = fok ? p.sb[(int64_t)(F + f + r) * p.sb_stride] : 0.0f;
-                    if (HAS_BIAS && fok) { bg[r] = load_bias(p.bias, f + r, 0); bu[r] = load_bias(p.bias, F + f + r, 0); }
-                }
+                for (int q = 0; q < 4; ++q) {
+                    const int cl = 32 * t + 8 * q + 4 * hi;
+                    const int f = col0 + cl;
+                    const bool ok = f < F && m < p.M;
+                    const v4f sbg = *reinterpret_cast<const v4f*>(sb_l + wn * 64 + cl);
+                    const v4f sbu = *reinterpret_cast<const v4f*>(sb_l + 128 + wn * 64 + cl);
+                    float bg[4] = {0, 0, 0, 0}, bu[4] = {0, 0, 0, 0};
+                    if (HAS_BIAS && f < F) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bool ok = fok && (mrow0 + 32 * j + mj < p.M);
-                    uint32_t hb[4];
+                        for (int r = 0; r < 4; ++r) {
+                            bg[r] = load_bias(p.bias, f + r, 0);
+                            bu[r] = load_bias(p.bias, F + f + r, 0);
+                        }
+                    }
+                    float hv[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float tg = sbg[r] * acc[t][j][4 * q + r];
                         const float tu = sbu[r] * acc[t + 2][j][4 * q + r];
-                        const float gy = HAS_BIAS ? __builtin_fmaf(sam[j], tg, bg[r]) : sam[j] * tg;
-                        const float uy = HAS_BIAS ? __builtin_fmaf(sam[j], tu, bu[r]) : sam[j] * tu;
-                        const uint32_t gb = bf16_rne(gy);
-                        float u = bf16_to_f32(bf16_rne(uy));
-                        u = (u == 0.0f) ? 0.0f : u;                       // -0 up -> +0 (fp8_swiglu.py:66)
-                        const float sl = bf16_to_f32(p.silu[gb]);
-                        hb[r] = bf16_rne(sl * u);
-                        const uint32_t ab = ok ? ((hb[r] & 0x7fffu) << 16) : 0u;
-                        rmax[j] = rmax[j] > ab ? rmax[j] : ab;
+                        const float gy = HAS_BIAS ? __builtin_fmaf(sam, tg, bg[r]) : sam * tg;
+                        const float uy = HAS_BIAS ? __builtin_fmaf(sam, tu, bu[r]) : sam * tu;
+                        const uint32_t gu = cvt_bf16x2(gy, uy);           // gate in the low half, up in the high
+                        const float u = zero_to_pos(u2f(gu & 0xffff0000u));   // -0 up -> +0 (fp8_swiglu.py:66)
+                        hv[r] = bf16_to_f32(p.silu[gu & 0xffffu]) * u;   // table of bf16(g / (1 + exp(-g)))
                     }
-                    put4(32 * j + mj, cl, hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+                    const uint32_t h01 = cvt_bf16x2(hv[0], hv[1]), h23 = cvt_bf16x2(hv[2], hv[3]);
+                    if (ok) rmax = max_abs_bf16x2(max_abs_bf16x2(rmax, h01), h23);
+                    put4(mj, cl, h01, h23);
                 }
             }
+            if (p.row_amax) row_amax(rmax, m);
+            flush(mrow0 + 32 * j, col0, F);
         }
     } else {
-        col0 = tile_n * BN + wn * 128;
-        ncols = p.N;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int cl = 32 * i + 8 * q + 4 * hi;
-                const int n = col0 + cl;
-                const bool nok = n < p.N;
-                float sbn[4], bn[4] = {0, 0, 0, 0};
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    sbn[r] = nok ? p.sb[(int64_t)(n + r) * p.sb_stride] : 0.0f;
-                    if (HAS_BIAS && nok) bn[r] = load_bias(p.bias, n + r, OUT_DT);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bool ok = nok && (mrow0 + 32 * j + mj < p.M);
-                    uint32_t o[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float t = sbn[r] * acc[i][j][4 * q + r];
-                        const float v = HAS_BIAS ? __builtin_fmaf(sam[j], t, bn[r]) : sam[j] * t;
-                        o[r] = OUT_DT ? fp16_rne(v) : bf16_rne(v);
-                        if (EPI == EPI_AMAX) {
-                            const uint32_t ab = ok ? ((o[r] & 0x7fffu) << 16) : 0u;
-                            rmax[j] = rmax[j] > ab ? rmax[j] : ab;
-                        }
-                    }
-                    put4(32 * j + mj, cl, o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-                }
-            }
-        }
-    }
-    if (EPI == EPI_AMAX || (EPI == EPI_SWIGLU && p.row_amax)) {
+        const int col0 = tn * BN + wn * 128;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint32_t v = rmax[j];
-            const uint32_t o = (uint32_t)__shfl_xor((int)v, 32, 64);
-            v = v > o ? v : o;
             const int m = mrow0 + 32 * j + mj;
-            if (hi == 0 && m < p.M && v) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, v);
+            const float sam = sa_l[wm * 128 + 32 * j + mj];
+            uint32_t rmax = 0;
+#pragma unroll
+            for (int ip = 0; ip < 2; ++ip) {
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii) {
+                    const int i = 2 * ip + ii;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int cl = 32 * ii + 8 * q + 4 * hi;          // column within the 64-wide pass
+                        const int n = col0 + 64 * ip + cl;
+                        const bool ok = n < p.N && m < p.M;
+                        const v4f sbn = *reinterpret_cast<const v4f*>(sb_l + wn * 128 + 64 * ip + cl);
+                        float bn[4] = {0, 0, 0, 0};
+                        if (HAS_BIAS && n < p.N) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) bn[r] = load_bias(p.bias, n + r, OUT_DT);
+                        }
+                        float v[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float t = sbn[r] * acc[i][j][4 * q + r];
+                            v[r] = HAS_BIAS ? __builtin_fmaf(sam, t, bn[r]) : sam * t;
+                        }
+                        uint32_t lo, hi2;
+                        if (OUT_DT) {
+                            lo = fp16_rne(v[0]) | (fp16_rne(v[1]) << 16);
+                            hi2 = fp16_rne(v[2]) | (fp16_rne(v[3]) << 16);
+                        } else {
+                            lo = cvt_bf16x2(v[0], v[1]);
+                            hi2 = cvt_bf16x2(v[2], v[3]);
+                        }
+                        if (EPI == EPI_AMAX && ok) rmax = max_abs_bf16x2(max_abs_bf16x2(rmax, lo), hi2);
+                        put4(mj, cl, lo, hi2);
+                    }
+                }
+                flush(mrow0 + 32 * j, col0 + 64 * ip, p.N);
+            }
+            if (EPI == EPI_AMAX) row_amax(rmax, m);
         }
     }
-    // the wave reads back its own tile (LDS accesses of one wave complete in order): 16 bytes per lane, CHUNKS lanes
-    // per row, whole row segments per store instruction
-    constexpr int ROWS_PER_PASS = 64 / CHUNKS;
-    const int c = lane % CHUNKS;
-    const int col = col0 + c * 8;
-    uint16_t* ybase = reinterpret_cast<uint16_t*>(p.y);
-#pragma unroll 4
-    for (int it = 0; it < 128 / ROWS_PER_PASS; ++it) {
-        const int ml = it * ROWS_PER_PASS + lane / CHUNKS;
-        const uint4 v = *reinterpret_cast<const uint4*>(tile + ml * ROW_BYTES + ((c ^ (ml & (CHUNKS - 1))) << 4));
-        const int m = mrow0 + ml;
-        if (m < p.M && col < ncols) *reinterpret_cast<uint4*>(ybase + (int64_t)m * p.ldy + col) = v;
-    }
 }
 
-template <int OUT_DT, bool HAS_BIAS, int EPI>
-__global__ void __launch_bounds__(256, 1) gemm_kernel(GemmParams p) {
-    gemm_body<OUT_DT, HAS_BIAS, EPI>(p, (int)blockIdx.x);
-}
+// Persistent kernel: workgroup b computes tiles b, b + G, b + 2G, ... (G = gridDim.x <= the CU count, one workgroup per
+// CU).  The load cursor runs two k-steps ahead of the MFMAs across tile boundaries, so the first two stages of the
+// next tile (and its scales) load while the current tile's last k-steps and epilogue run.
+template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED>
+__global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_TOTAL];
 
-struct GroupedParams {
-    GemmParams g[H3FP8_MAX_GROUPS];
-    int n;
-};
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave & 1, wm = wave >> 1;
+    const int G = (int)gridDim.x;
 
-// One launch over the concatenated tile spaces of up to H3FP8_MAX_GROUPS problems (bf16 out, no bias).
-__global__ void __launch_bounds__(256, 1) gemm_grouped_kernel(GroupedParams gp) {
-    const int b = (int)blockIdx.x;
-    int i = 0;
+    Cursor I;
+    cursor_set<EPI, GROUPED>(I, gp, 0, wave, lane);
+    if (!I.valid) return;
+
+    // prologue: k-steps 0 and 1 (and the scales of their tiles) in flight, the sub-step-0 fragments of k-step 0 in
+    // registers; every load group is 16 stage loads followed by 2 scale loads
+    v8i fa0[4], fb0[4], fa1[4], fb1[4];
+    const uint32_t lds0 = lds_addr(lds);
+    issue_stage<EPI>(lds0, I, wave);
+    issue_scales(lds0, I, wave);
+    cursor_next<EPI, GROUPED>(I, gp, wave, lane);
+    issue_stage<EPI>(lds0 + STAGE_BYTES, I, wave);
+    issue_scales(lds0, I, wave);
+    if (I.valid) cursor_next<EPI, GROUPED>(I, gp, wave, lane);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(18));
+    barrier_nofence();
+    read_frags<EPI>(lds, wn, wm, lane, 0, fa0, fb0);
+
+    int g = 0;
+    for (int c = 0;; ++c) {
+        const int id = (int)blockIdx.x + c * G;
+        int tm, tn;
+        const int pi = locate<GROUPED>(gp, id, tm, tn);
+        const GemmParams& p = gp.g[pi];
+        const int nk = (p.K + BK - 1) / BK;
+
+        v16f acc[4][4];
 #pragma unroll
-    for (int j = 1; j < H3FP8_MAX_GROUPS; ++j)
-        if (j < gp.n && b >= gp.g[j].tile_offset) i = j;
-    gemm_body<0, false, EPI_PLAIN>(gp.g[i], b - gp.g[i].tile_offset);
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+        for (int ks = 0; ks < nk; ++ks, ++g) {
+            kstep<EPI>(lds, lds0, g, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+            if (I.valid) cursor_next<EPI, GROUPED>(I, gp, wave, lane);
+        }
+        epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
+        if (id + G >= gp.total_tiles) break;
+    }
+    wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
 }
 
 __global__ void __launch_bounds__(256) fill_zero_kernel(float* p, int64_t n) {
@@ -526,25 +653,29 @@ int zero_rows(float* p, int64_t n, hipStream_t st) {
     return H3FP8_OK;
 }
 
-template <int OUT_DT, bool HAS_BIAS, int EPI>
-int launch_one(const GemmParams& p, int blocks, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI>), dim3(blocks), dim3(256), 0, st, p);
+// Workgroups of a persistent launch over `tiles` tiles: one per CU, at most one per tile.
+int grid_for(int tiles) { return std::max(1, std::min(tiles, h3host::cu_count())); }
+
+template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED>
+int launch_one(const GroupedParams& gp, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI, GROUPED>), dim3(grid_for(gp.total_tiles)), dim3(256), 0, st,
+                       gp);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
 
 template <int EPI>
-int dispatch(const GemmParams& p, int out_dt, bool has_bias, int blocks, hipStream_t st) {
+int dispatch(const GroupedParams& gp, int out_dt, bool has_bias, hipStream_t st) {
     if (out_dt == H3FP8_DT_BF16) {
-        return has_bias ? launch_one<0, true, EPI>(p, blocks, st) : launch_one<0, false, EPI>(p, blocks, st);
+        return has_bias ? launch_one<0, true, EPI, false>(gp, st) : launch_one<0, false, EPI, false>(gp, st);
     }
-    if (out_dt == H3FP8_DT_F32) return launch_one<H3FP8_DT_F32, false, EPI_PLAIN>(p, blocks, st);
-    return has_bias ? launch_one<1, true, EPI>(p, blocks, st) : launch_one<1, false, EPI>(p, blocks, st);
+    if (out_dt == H3FP8_DT_F32) return launch_one<H3FP8_DT_F32, false, EPI_PLAIN, false>(gp, st);
+    return has_bias ? launch_one<1, true, EPI, false>(gp, st) : launch_one<1, false, EPI, false>(gp, st);
 }
 
 constexpr int64_t kMaxBufferBytes = 0x7fff0000LL;   // buffer offsets are 32-bit; keep clear of the OOB marker
 
-// Common argument checks; fills the fields that do not depend on the M range.
+// Common argument checks.
 int check_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const float* sa, int64_t sa_stride,
                const float* sb, int64_t sb_stride, const void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                int64_t w_rows, const char* who) {
@@ -559,8 +690,10 @@ int check_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const flo
     H3_REQUIRE(ldy >= N && ldy % 8 == 0, "%s: ldy must be >= N and a multiple of 8", who);
     H3_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)y & 15) == 0,
                "%s: a, w and y must be 16-byte aligned", who);
+    H3_REQUIRE(((uintptr_t)sa & 3) == 0 && ((uintptr_t)sb & 3) == 0, "%s: scales must be 4-byte aligned", who);
     H3_REQUIRE(sa_stride >= 0 && sb_stride >= 0, "%s: negative scale stride", who);
     H3_REQUIRE((w_rows - 1) * ldw + K <= kMaxBufferBytes, "%s: weight too large for one buffer range", who);
+    H3_REQUIRE((w_rows - 1) * sb_stride * 4 + 4 <= kMaxBufferBytes, "%s: sb too large", who);
     H3_REQUIRE(lda * 512 <= kMaxBufferBytes, "%s: lda too large", who);
     return H3FP8_OK;
 }
@@ -574,6 +707,7 @@ GemmParams make_params(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t 
     p.lda = lda; p.ldw = ldw; p.ldy = ldy;
     p.sa_stride = sa_stride; p.sb_stride = sb_stride;
     p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    p.w_rows = (int)w_rows;
     p.a_bytes = (uint32_t)((M - 1) * lda + K);
     p.w_bytes = (uint32_t)((w_rows - 1) * ldw + K);
     const int64_t n_tile_cols = swiglu ? (BN / 2) : BN;
@@ -584,22 +718,26 @@ GemmParams make_params(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t 
     return p;
 }
 
-// Launches one problem, splitting M so that every launch's activation range fits a 32-bit buffer offset.
+// Launches one problem, splitting M so that every launch's activation and scale ranges fit 32-bit buffer offsets.
 int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, const float* sa,
              int64_t sa_stride, const float* sb, int64_t sb_stride, const void* bias, void* y, int64_t ldy,
              int out_dt, int64_t M, int64_t N, int64_t K, int64_t w_rows, float* row_amax, const uint16_t* silu,
              hipStream_t st) {
-    const int64_t rows_per = std::max<int64_t>(BM, ((kMaxBufferBytes - K) / lda + 1) / BM * BM);
+    int64_t rows_per = std::max<int64_t>(BM, ((kMaxBufferBytes - K) / lda + 1) / BM * BM);
+    if (sa_stride > 0) rows_per = std::min<int64_t>(rows_per, std::max<int64_t>(BM, kMaxBufferBytes / (4 * sa_stride) / BM * BM));
+    const int out_elem = (out_dt == H3FP8_DT_F32) ? 4 : 2;
     for (int64_t r0 = 0; r0 < M; r0 += rows_per) {
         const int64_t Mi = std::min<int64_t>(rows_per, M - r0);
-        GemmParams p = make_params(a + r0 * lda, lda, w, ldw, sa + r0 * sa_stride, sa_stride, sb, sb_stride, bias,
-                                   reinterpret_cast<uint16_t*>(y) + r0 * ldy, ldy, Mi, N, K, w_rows,
-                                   row_amax ? row_amax + r0 : nullptr, silu, epi == EPI_SWIGLU);
-        const int blocks = p.tiles_m * p.tiles_n;
+        GroupedParams gp{};
+        gp.g[0] = make_params(a + r0 * lda, lda, w, ldw, sa + r0 * sa_stride, sa_stride, sb, sb_stride, bias,
+                              reinterpret_cast<uint8_t*>(y) + r0 * ldy * out_elem, ldy, Mi, N, K, w_rows,
+                              row_amax ? row_amax + r0 : nullptr, silu, epi == EPI_SWIGLU);
+        gp.n = 1;
+        gp.total_tiles = gp.g[0].tiles_m * gp.g[0].tiles_n;
         int rc;
-        if (epi == EPI_PLAIN) rc = dispatch<EPI_PLAIN>(p, out_dt, bias != nullptr, blocks, st);
-        else if (epi == EPI_AMAX) rc = dispatch<EPI_AMAX>(p, out_dt, bias != nullptr, blocks, st);
-        else rc = dispatch<EPI_SWIGLU>(p, H3FP8_DT_BF16, bias != nullptr, blocks, st);
+        if (epi == EPI_PLAIN) rc = dispatch<EPI_PLAIN>(gp, out_dt, bias != nullptr, st);
+        else if (epi == EPI_AMAX) rc = dispatch<EPI_AMAX>(gp, out_dt, bias != nullptr, st);
+        else rc = dispatch<EPI_SWIGLU>(gp, H3FP8_DT_BF16, bias != nullptr, st);
         if (rc) return rc;
     }
     return H3FP8_OK;
@@ -624,6 +762,8 @@ int h3fp8_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const flo
     H3_REQUIRE(out_dtype != H3FP8_DT_F32 || (!bias && !row_amax && ldy % 4 == 0),
                "h3fp8_gemm: the fp32 accumulator probe takes no bias or row_amax and needs ldy %% 4 == 0");
     if (M == 0 || N == 0) return H3FP8_OK;
+    rc = h3host::ensure_device_init();
+    if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     if (row_amax) {
         rc = zero_rows(row_amax, M, st);
@@ -675,7 +815,7 @@ int h3fp8_gemm_swiglu_quant(const void* a, int64_t lda, const void* w_gate_up, i
 int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream) {
     H3_REQUIRE(groups && n_groups >= 0 && n_groups <= H3FP8_MAX_GROUPS, "h3fp8_grouped_gemm: bad group list");
     GroupedParams gp{};
-    int blocks = 0;
+    int tiles = 0;
     for (int i = 0; i < n_groups; ++i) {
         const h3fp8_group& g = groups[i];
         int rc = check_gemm(g.a, g.lda, g.w, g.ldw, g.sa, g.sa_stride, g.sb, g.sb_stride, g.y, g.ldy, g.M, g.N, g.K,
@@ -683,17 +823,20 @@ int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream) {
         if (rc) return rc;
         H3_REQUIRE(g.M == 0 || (g.M - 1) * g.lda + g.K <= kMaxBufferBytes,
                    "h3fp8_grouped_gemm: group %d activation too large for one launch", i);
+        H3_REQUIRE(g.M == 0 || (g.M - 1) * g.sa_stride * 4 + 4 <= kMaxBufferBytes,
+                   "h3fp8_grouped_gemm: group %d scales too large for one launch", i);
         if (g.M == 0 || g.N == 0) continue;
         GemmParams p = make_params((const uint8_t*)g.a, g.lda, (const uint8_t*)g.w, g.ldw, g.sa, g.sa_stride, g.sb,
                                    g.sb_stride, nullptr, g.y, g.ldy, g.M, g.N, g.K, g.N, nullptr, nullptr, false);
-        p.tile_offset = blocks;
-        blocks += p.tiles_m * p.tiles_n;
+        p.tile_offset = tiles;
+        tiles += p.tiles_m * p.tiles_n;
         gp.g[gp.n++] = p;
     }
-    if (blocks == 0) return H3FP8_OK;
-    hipLaunchKernelGGL(gemm_grouped_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, gp);
-    H3_CHECK_HIP(hipGetLastError());
-    return H3FP8_OK;
+    if (tiles == 0) return H3FP8_OK;
+    gp.total_tiles = tiles;
+    int rc = h3host::ensure_device_init();
+    if (rc) return rc;
+    return launch_one<0, false, EPI_PLAIN, true>(gp, (hipStream_t)stream);
 }
 
 }  // extern "C"

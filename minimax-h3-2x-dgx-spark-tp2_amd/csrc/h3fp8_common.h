@@ -45,6 +45,15 @@ __device__ __forceinline__ uint32_t fp16_rne(float f) {
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return u2f(h << 16); }
 
+// Two fp32 -> packed bf16 (a in the low half), round to nearest even: gfx950's v_cvt_pk_bf16_f32.  It equals bf16_rne
+// above on every fp32 input, NaN payloads included (checked over all 2^32 inputs by h3fp8_selfcheck_bf16).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+    const f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ float fp16_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 // Software fp32 -> OCP e4m3fn (round to nearest even, >= 480 and NaN -> 0x7f | sign): the bit rule of torch's
@@ -124,6 +133,7 @@ void set_error(const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 int ensure_device_init();                      // per-device one-time set-up (SiLU table); returns status
 const uint16_t* silu_table_ptr();              // device address of the current device's SiLU table
+int cu_count();                                // compute units of the current device (after ensure_device_init)
 }  // namespace h3host
 
 #define H3_CHECK_HIP(call)                                              \

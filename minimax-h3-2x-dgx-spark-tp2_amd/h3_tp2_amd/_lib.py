@@ -48,6 +48,7 @@ _SIGS = {
     "h3fp8_scale_bias_cast": ([P, I64, P, I64, P, I64, P, P, I64, I, I64, I64, P], I),
     "h3fp8_grouped_gemm": ([ctypes.POINTER(Group), I, P], I),
     "h3fp8_selfcheck_e4m3": ([ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], I),
+    "h3fp8_selfcheck_bf16": ([ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], I),
     "h3fp8_copy_silu_table": ([P, P], I),
 }
 

@@ -270,6 +270,14 @@ def selfcheck_e4m3() -> tuple[int, int]:
     return int(bad.value), int(nan_bad.value)
 
 
+def selfcheck_bf16() -> tuple[int, int]:
+    """(non-NaN mismatches, NaN inputs not mapped to NaN) of the hardware bf16 pair conversion against the RNE rule,
+    over every fp32 bit pattern (synchronous)."""
+    bad, nan_bad = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    _lib.call("h3fp8_selfcheck_bf16", ctypes.byref(bad), ctypes.byref(nan_bad))
+    return int(bad.value), int(nan_bad.value)
+
+
 def silu_table(device=None) -> torch.Tensor:  # noqa: ANN001
     """The device's SiLU table (65536 bf16 bit patterns as int16)."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)

@@ -295,3 +295,4 @@ def test_dequant_matmul_k_ascending_fp32():
     for k in range(96):                                   # fp32, one rounding per multiply and per add, k ascending
         ref = (ref + (a[:, k:k + 1] * w[None, :, k]).astype(np.float32)).astype(np.float32)
     assert np.array_equal(O.dequant_matmul(ac, wc), ref)
+

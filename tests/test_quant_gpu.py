@@ -30,6 +30,12 @@ def test_hw_e4m3_conversion_matches_torch_rule(cuda):
     assert bad == 0 and nan_bad == 0, (bad, nan_bad)
 
 
+def test_hw_bf16_conversion_matches_rne(cuda):
+    """The epilogues' hardware fp32 -> bf16 pair conversion equals the RNE rule on all 2^32 fp32 patterns."""
+    from h3_tp2_amd import ops
+    assert ops.selfcheck_bf16() == (0, 0)
+
+
 @pytest.mark.parametrize("M,K", [(1, 16), (3, 512), (200, 3072), (333, 5376), (64, 8192), (17, 14336), (5, 20480),
                                  (1000, 1536), (31, 4096), (7, 1040), (129, 7168), (2, 18432)])
 @pytest.mark.parametrize("kind", ["normal", "lognormal"])
