@@ -380,7 +380,7 @@ constexpr bool DMA_SPREAD = true;
 // weight tile t / 4 and token tile t % 4, so reading weight tile 0 and then the token tiles lets it start earliest
 constexpr int NEXT_READ_ORDER[8] = {0, 4, 5, 6, 7, 1, 2, 3};
 
-template <int EPI>
+template <int EPI, bool READ_NEXT>
 __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, int wave, int wn, int wm,
                                       int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4], v8i fb1[4]) {
     uint8_t* cur = lds + (g & 1) * STAGE_BYTES;
@@ -410,7 +410,7 @@ __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const 
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(BEFORE));   // k-step g+1 (and everything older) has landed
             barrier_nofence();
         }
-        if (t >= MFMA_SPLIT) {
+        if (READ_NEXT && t >= MFMA_SPLIT) {
             // spread the 8 fragment reads of k-step g+1 over the MFMAs after barrier 2
             constexpr int PER = (8 + (16 - MFMA_SPLIT) - 1) / (16 - MFMA_SPLIT);
 #pragma unroll
@@ -479,12 +479,22 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
     auto flush = [&](int m0, int col0, int ncols) {
         const int c = lane & 7;
         const int col = col0 + c * 8;
+        uint4 v[4];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
+        for (int it = 0; it < 4; ++it) {                // all four reads before the first store
             const int ml = it * 8 + (lane >> 3);
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
-            const int m = m0 + ml;
-            if (m < p.M && col < ncols) *reinterpret_cast<uint4*>(ybase + (int64_t)m * p.ldy + col) = v;
+            v[it] = *reinterpret_cast<const uint4*>(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+        }
+        uint16_t* yrow = ybase + (int64_t)(m0 + (lane >> 3)) * p.ldy + col;
+        if (m0 + 32 <= p.M && col0 + 64 <= ncols) {     // whole 32 x 64 piece in range (uniform): no per-row test
+#pragma unroll
+            for (int it = 0; it < 4; ++it) *reinterpret_cast<uint4*>(yrow + (int64_t)(it * 8) * p.ldy) = v[it];
+        } else {
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int m = m0 + it * 8 + (lane >> 3);
+                if (m < p.M && col < ncols) *reinterpret_cast<uint4*>(yrow + (int64_t)(it * 8) * p.ldy) = v[it];
+            }
         }
     };
     auto row_amax = [&](uint32_t v, int m) {
@@ -495,20 +505,30 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
     if (EPI == EPI_SWIGLU) {
         const int F = p.N;
         const int col0 = tn * (BN / 2) + wn * 64;
+        // every scale the wave needs, read once up front (one LDS round trip instead of one per group of four)
+        float sa_j[4];
+        v4f sbg_v[2][4], sbu_v[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sa_j[j] = sa_l[wm * 128 + 32 * j + mj];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sbg_v[t][q] = *reinterpret_cast<const v4f*>(sb_l + wn * 64 + 32 * t + 8 * q + 4 * hi);
+                sbu_v[t][q] = *reinterpret_cast<const v4f*>(sb_l + 128 + wn * 64 + 32 * t + 8 * q + 4 * hi);
+            }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = mrow0 + 32 * j + mj;
-            const float sam = sa_l[wm * 128 + 32 * j + mj];
-            uint32_t rmax = 0;
+            const float sam = sa_j[j];
+            // gate and up of the pass rounded to bf16 (packed: gate low, up high), then every SiLU lookup of the pass
+            // issued before the first is used (one round trip to the table per pass)
+            uint32_t gu[2][4][4], sl[2][4][4];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int cl = 32 * t + 8 * q + 4 * hi;
-                    const int f = col0 + cl;
-                    const bool ok = f < F && m < p.M;
-                    const v4f sbg = *reinterpret_cast<const v4f*>(sb_l + wn * 64 + cl);
-                    const v4f sbu = *reinterpret_cast<const v4f*>(sb_l + 128 + wn * 64 + cl);
+                    const int f = col0 + 32 * t + 8 * q + 4 * hi;
                     float bg[4] = {0, 0, 0, 0}, bu[4] = {0, 0, 0, 0};
                     if (HAS_BIAS && f < F) {
 #pragma unroll
@@ -517,16 +537,33 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                             bu[r] = load_bias(p.bias, F + f + r, 0);
                         }
                     }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float tg = sbg_v[t][q][r] * acc[t][j][4 * q + r];
+                        const float tu = sbu_v[t][q][r] * acc[t + 2][j][4 * q + r];
+                        const float gy = HAS_BIAS ? __builtin_fmaf(sam, tg, bg[r]) : sam * tg;
+                        const float uy = HAS_BIAS ? __builtin_fmaf(sam, tu, bu[r]) : sam * tu;
+                        gu[t][q][r] = cvt_bf16x2(gy, uy);
+                    }
+                }
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sl[t][q][r] = p.silu[gu[t][q][r] & 0xffffu];   // bf16(g/(1+exp(-g)))
+            uint32_t rmax = 0;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int cl = 32 * t + 8 * q + 4 * hi;
+                    const bool ok = col0 + cl < F && m < p.M;
                     float hv[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float tg = sbg[r] * acc[t][j][4 * q + r];
-                        const float tu = sbu[r] * acc[t + 2][j][4 * q + r];
-                        const float gy = HAS_BIAS ? __builtin_fmaf(sam, tg, bg[r]) : sam * tg;
-                        const float uy = HAS_BIAS ? __builtin_fmaf(sam, tu, bu[r]) : sam * tu;
-                        const uint32_t gu = cvt_bf16x2(gy, uy);           // gate in the low half, up in the high
-                        const float u = zero_to_pos(u2f(gu & 0xffff0000u));   // -0 up -> +0 (fp8_swiglu.py:66)
-                        hv[r] = bf16_to_f32(p.silu[gu & 0xffffu]) * u;   // table of bf16(g / (1 + exp(-g)))
+                        const float u = zero_to_pos(u2f(gu[t][q][r] & 0xffff0000u));   // -0 up -> +0 (fp8_swiglu.py:66)
+                        hv[r] = bf16_to_f32(sl[t][q][r]) * u;
                     }
                     const uint32_t h01 = cvt_bf16x2(hv[0], hv[1]), h23 = cvt_bf16x2(hv[2], hv[3]);
                     if (ok) rmax = max_abs_bf16x2(max_abs_bf16x2(rmax, h01), h23);
@@ -538,10 +575,19 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
         }
     } else {
         const int col0 = tn * BN + wn * 128;
+        // every scale the wave needs, read once up front (one LDS round trip instead of one per group of four)
+        float sa_j[4];
+        v4f sb_v[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sa_j[j] = sa_l[wm * 128 + 32 * j + mj];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sb_v[i][q] = *reinterpret_cast<const v4f*>(sb_l + wn * 128 + 32 * i + 8 * q + 4 * hi);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = mrow0 + 32 * j + mj;
-            const float sam = sa_l[wm * 128 + 32 * j + mj];
+            const float sam = sa_j[j];
             uint32_t rmax = 0;
 #pragma unroll
             for (int ip = 0; ip < 2; ++ip) {
@@ -553,7 +599,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                         const int cl = 32 * ii + 8 * q + 4 * hi;          // column within the 64-wide pass
                         const int n = col0 + 64 * ip + cl;
                         const bool ok = n < p.N && m < p.M;
-                        const v4f sbn = *reinterpret_cast<const v4f*>(sb_l + wn * 128 + 64 * ip + cl);
+                        const v4f sbn = sb_v[i][q];
                         float bn[4] = {0, 0, 0, 0};
                         if (HAS_BIAS && n < p.N) {
 #pragma unroll
@@ -631,12 +677,18 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-        for (int ks = 0; ks < nk; ++ks, ++g) {
-            kstep<EPI>(lds, lds0, g, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        for (int ks = 0; ks < nk - 1; ++ks, ++g) {
+            kstep<EPI, true>(lds, lds0, g, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
             if (I.valid) cursor_next<EPI, GROUPED>(I, gp, wave, lane);
         }
+        // the tile's last k-step publishes the next k-step's stage but leaves its fragment registers free for the
+        // epilogue; they are read after it
+        kstep<EPI, false>(lds, lds0, g, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        if (I.valid) cursor_next<EPI, GROUPED>(I, gp, wave, lane);
+        ++g;
         epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
         if (id + G >= gp.total_tiles) break;
+        read_frags<EPI>(lds + (g & 1) * STAGE_BYTES, wn, wm, lane, 0, fa0, fb0);
     }
     wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
 }
