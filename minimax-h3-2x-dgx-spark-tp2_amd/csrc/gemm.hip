@@ -50,7 +50,6 @@ constexpr int ROWB = BK;         // bytes per LDS row
 constexpr int STAGE_BYTES = (BM + BN) * ROWB;   // 64 KiB
 constexpr int NSTAGE = 2;
 constexpr int A_REGION = BN * ROWB;             // activation rows start after the weight rows
-constexpr int MFMA_SPLIT = 10;                  // sub-step-1 MFMAs issued before the stage barrier (of 16)
 constexpr uint32_t OOB = 0x80000000u;         // an offset past every buffer's range: the load returns zeros
 
 enum Epi { EPI_PLAIN = 0, EPI_AMAX = 1, EPI_SWIGLU = 2 };
@@ -368,53 +367,53 @@ __device__ __forceinline__ void cursor_next(Cursor& I, const GroupedParams& gp, 
 // the cursor points at k-step g+2, possibly of the next tile).  The instruction stream is the same for every k-step:
 // when there is no k-step g+2 the 16 loads are issued with out-of-range offsets (they fill the freed stage with zeros
 // and touch no memory), the two scale loads go to a scratch slot of the LDS unless g+2 starts a tile, and after the
-// last k-step the extra fragment reads of the other stage are simply not used.
-//   phase A: the 16 sub-step-0 MFMAs, with the reads of the 8 sub-step-1 fragments issued between the first 8;
-//   barrier 1 (after lgkmcnt(0)): every wave's reads of this stage have returned -- the stage is free;
-//   phase B: the 16 sub-step-1 MFMAs, with the 16 load instructions of k-step g+2 into the freed stage issued one per
-//   MFMA (DMA_SPREAD) or two per MFMA over the first 8, then the two scale loads; once this wave's share of k-step g+1
-//   has landed (vmcnt: only the instructions issued in this phase may be outstanding), barrier 2 publishes it and the
-//   sub-step-0 fragments of g+1 are read between the last 16 - MFMA_SPLIT MFMAs.
-constexpr bool DMA_SPREAD = true;
+// last k-step the extra fragment reads of the other stage are simply not used.  Loads are issued one per MFMA: issued
+// in bursts they stall the wave's instruction stream and with it the matrix core.
 // order of the next k-step's sub-step-0 fragment reads (0..3 weight tiles, 4..7 token tiles): MFMA t of phase A uses
 // weight tile t / 4 and token tile t % 4, so reading weight tile 0 and then the token tiles lets it start earliest
 constexpr int NEXT_READ_ORDER[8] = {0, 4, 5, 6, 7, 1, 2, 3};
+
+// Schedule of one k-step over its 32 MFMAs (u = 0..15: sub-step 0, u = 16..31: sub-step 1):
+//   u < 8        the 8 sub-step-1 fragment reads of stage g, one per MFMA;
+//   u == REL     lgkmcnt(0) + barrier 1: every wave's reads of stage g have returned -- the stage is free;
+//   REL < u      the 16 load instructions of k-step g+2 into the freed stage, one per MFMA, and the two scale loads
+//                after the eighth;
+//   u == PUB     vmcnt + barrier 2: k-step g+1 has landed (only loads issued in this k-step may be outstanding);
+//   u > PUB      the 8 sub-step-0 fragment reads of k-step g+1 (READ_NEXT), in the order its first MFMAs use them.
+constexpr int KS_REL = 9;                      // measured best of 9..15 (QKV and K = 8192 shapes)
+constexpr int KS_PUB = 26;
+static_assert(KS_REL >= 7 && KS_REL + 16 <= 31 && KS_PUB > KS_REL && KS_PUB < 31, "k-step schedule");
+constexpr int ks_loads_before_pub() {
+    const int stage = (KS_PUB - KS_REL) < 16 ? (KS_PUB - KS_REL) : 16;
+    return stage + (KS_REL + 9 <= KS_PUB ? 2 : 0);
+}
 
 template <int EPI, bool READ_NEXT>
 __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, int wave, int wn, int wm,
                                       int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4], v8i fb1[4]) {
     uint8_t* cur = lds + (g & 1) * STAGE_BYTES;
     uint8_t* nxt = lds + ((g + 1) & 1) * STAGE_BYTES;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        mfma_one(acc, fa0, fb0, t);
-        if (t < 8) read_one<EPI>(cur, wn, wm, lane, 1, t, fa1, fb1);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    wait_lgkm0();                                       // this wave's reads of stage g & 1 have returned
-    barrier_nofence();                                  // ... and every wave's: the stage is free
     const StageIssue S = stage_issue<EPI>(lds0 + (uint32_t)(g & 1) * STAGE_BYTES, I, wave);
-    // load instructions issued before the vmcnt wait of MFMA MFMA_SPLIT - 1
-    constexpr int BEFORE = (DMA_SPREAD ? MFMA_SPLIT : 16) + 2;
+    constexpr int NREAD = 31 - KS_PUB;                  // MFMAs that carry the next k-step's reads
+    constexpr int PER = (8 + NREAD - 1) / NREAD;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        mfma_one(acc, fa1, fb1, t);
-        if (DMA_SPREAD) {
-            issue_one<EPI>(S, I.L, t);
-        } else if (t < 8) {
-            issue_one<EPI>(S, I.L, 2 * t);
-            issue_one<EPI>(S, I.L, 2 * t + 1);
+    for (int u = 0; u < 32; ++u) {
+        if (u < 16) mfma_one(acc, fa0, fb0, u);
+        else mfma_one(acc, fa1, fb1, u - 16);
+        if (u < 8) read_one<EPI>(cur, wn, wm, lane, 1, u, fa1, fb1);
+        if (u == KS_REL) {
+            wait_lgkm0();                               // this wave's reads of stage g & 1 have returned
+            barrier_nofence();                          // ... and every wave's: the stage is free
         }
-        if (t == 8) issue_scales(lds0, I, wave);
-        if (t == MFMA_SPLIT - 1) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(BEFORE));   // k-step g+1 (and everything older) has landed
+        if (u > KS_REL && u <= KS_REL + 16) issue_one<EPI>(S, I.L, u - KS_REL - 1);
+        if (u == KS_REL + 9) issue_scales(lds0, I, wave);
+        if (u == KS_PUB) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(ks_loads_before_pub()));   // k-step g+1 (and older) has landed
             barrier_nofence();
         }
-        if (READ_NEXT && t >= MFMA_SPLIT) {
-            // spread the 8 fragment reads of k-step g+1 over the MFMAs after barrier 2
-            constexpr int PER = (8 + (16 - MFMA_SPLIT) - 1) / (16 - MFMA_SPLIT);
+        if (READ_NEXT && u > KS_PUB) {
 #pragma unroll
-            for (int f = (t - MFMA_SPLIT) * PER; f < (t - MFMA_SPLIT + 1) * PER; ++f)
+            for (int f = (u - KS_PUB - 1) * PER; f < (u - KS_PUB) * PER; ++f)
                 if (f < 8) read_one<EPI>(nxt, wn, wm, lane, 0, NEXT_READ_ORDER[f], fa0, fb0);
         }
         __builtin_amdgcn_sched_barrier(0);
