@@ -68,6 +68,7 @@ struct GemmParams {
     int M, N, K;               // SwiGLU: N = F (output width)
     int w_rows;                // rows of w and entries of sb (N, or 2F for SwiGLU)
     uint32_t a_bytes, w_bytes; // buffer ranges
+    uint32_t y_bytes;          // output range: ((M - 1) * ldy + N) * element size; stores past it are dropped
     int tiles_m, tiles_n;
     int group_m;
     int tile_offset;           // grouped launches: first block of this problem
@@ -178,10 +179,9 @@ struct Loader {
     v4u rw, ra;                 // weight / activation buffer descriptors
     v4u rsa, rsb;               // scale buffer descriptors
     uint32_t vw[2], va[2];      // lane part of the byte offsets for even / odd instructions (OOB: share out of range)
-    uint32_t c16[2];            // 16 * logical chunk of this lane for even / odd instructions
+    uint32_t vw_t[2], va_t[2];  // the same for the tile's last k-step: OOB where the lane's chunk lies at or past K
     uint32_t row8_w, row8_a;    // byte advance of 8 rows
     uint32_t sa_off, sb_off;    // this lane's scale offsets (OOB past the range)
-    int K;
     int w_groups;               // SwiGLU: 8-row groups of this wave's weight share that are in range
 };
 
@@ -276,15 +276,19 @@ __device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn,
     const int64_t arow0 = (int64_t)tm * BM + 64 * wave;
     L.rw = buffer_desc(p.w, p.w_bytes);
     L.ra = buffer_desc(p.a, p.a_bytes);
+    // bytes of k that the tile's last k-step covers (0: all BK); chunks at or past it read zeros in that k-step
+    const uint32_t ktail = (uint32_t)(p.K % BK);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-        L.c16[e] = 16u * lch[e];
-        L.vw[e] = (wrow0 >= wlimit) ? OOB : (uint32_t)((wrow0 + lrow) * p.ldw) + L.c16[e];
-        L.va[e] = (arow0 >= p.M) ? OOB : (uint32_t)((arow0 + lrow) * p.lda) + L.c16[e];
+        const uint32_t c16 = 16u * lch[e];
+        L.vw[e] = (wrow0 >= wlimit) ? OOB : (uint32_t)((wrow0 + lrow) * p.ldw) + c16;
+        L.va[e] = (arow0 >= p.M) ? OOB : (uint32_t)((arow0 + lrow) * p.lda) + c16;
+        const bool cut = ktail != 0 && c16 >= ktail;
+        L.vw_t[e] = cut ? OOB : L.vw[e];
+        L.va_t[e] = cut ? OOB : L.va[e];
     }
     L.row8_w = (uint32_t)(8 * p.ldw);
     L.row8_a = (uint32_t)(8 * p.lda);
-    L.K = p.K;
     // Partial shares rely on the descriptor's range check (rows >= M or >= N start past the last valid byte), except
     // SwiGLU gate rows past F, which would read up rows: those 8-row groups are zero-filled (F % 16 == 0).
     L.w_groups = (int)min<int64_t>(8, max<int64_t>(0, (wlimit - wrow0 + 7) / 8));
@@ -298,21 +302,33 @@ __device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn,
     L.sb_off = (wr < wlimit) ? (uint32_t)(wr * p.sb_stride * 4) : OOB;
 }
 
-// The load-issue cursor: the (tile, k-step) whose operands are loaded next, two k-steps ahead of the MFMAs.
+// The load-issue cursor: the (tile, k-step) whose operands are loaded next, two k-steps ahead of the MFMAs.  Everything
+// a k-step's loads need is prepared per tile here, so that the k-step itself adds only k0 to four offsets.
 struct Cursor {
     Loader L;
     int c;          // workgroup-local tile ordinal (global tile id = blockIdx.x + c * gridDim.x)
     int ks, nk;
     bool valid;
+    uint32_t dsa, dsb;  // LDS addresses of this wave's share of the tile's scale set (set c % NSCALE)
 };
 
 template <int EPI, bool GROUPED>
-__device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, int c, int wave, int lane) {
+__device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, int c, uint32_t lds0, int wave,
+                                           int lane) {
     const int id = (int)blockIdx.x + c * (int)gridDim.x;
     I.c = c;
     I.ks = 0;
     I.valid = id < gp.total_tiles;
-    if (!I.valid) return;
+    I.dsa = lds0 + SCALES_OFF + (uint32_t)(c % NSCALE) * SCALE_SET + 256u * (uint32_t)wave;
+    I.dsb = I.dsa + 1024u;
+    if (!I.valid) {
+        // past the last tile: the loads still run (every k-step has the same instruction stream and wait counts),
+        // read nothing and fill the stage with zeros
+#pragma unroll
+        for (int e = 0; e < 2; ++e) I.L.vw[e] = I.L.va[e] = I.L.vw_t[e] = I.L.va_t[e] = OOB;
+        I.nk = 1;
+        return;
+    }
     int tm, tn;
     const int pi = locate<GROUPED>(gp, id, tm, tn);
     const GemmParams& p = gp.g[pi];
@@ -320,28 +336,26 @@ __device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, i
     make_loader<EPI>(p, tm, tn, wave, lane, I.L);
 }
 
-// The load instructions of the cursor's k-step for this wave.  Past the last tile every offset is out of range: the
-// loads still run (so that every k-step has the same instruction stream and wait counts) and fill the stage with zeros.
+// The load instructions of the cursor's k-step for this wave (wofs = the wave's 64-row share within a region).
 template <int EPI>
-__device__ __forceinline__ StageIssue stage_issue(uint32_t stage, const Cursor& I, int wave) {
+__device__ __forceinline__ StageIssue stage_issue(uint32_t stage, const Cursor& I, uint32_t wofs) {
     const Loader& L = I.L;
     StageIssue S;
     const uint32_t k0 = (uint32_t)I.ks * BK;
-    const bool tail = (int)k0 + BK > L.K;                      // K tail: chunks at or past K read zeros
+    const bool last = I.ks == I.nk - 1;                         // uniform: the K tail, if any, is in this k-step
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-        const bool dead = !I.valid || (tail && (k0 + L.c16[e]) >= (uint32_t)L.K);
-        S.vw[e] = dead ? OOB : L.vw[e] + k0;
-        S.va[e] = dead ? OOB : L.va[e] + k0;
+        S.vw[e] = (last ? L.vw_t[e] : L.vw[e]) + k0;
+        S.va[e] = (last ? L.va_t[e] : L.va[e]) + k0;
     }
-    S.wdst = __builtin_amdgcn_readfirstlane(stage + wave * 64 * ROWB);       // wave-uniform: an SGPR for m0
-    S.adst = __builtin_amdgcn_readfirstlane(stage + A_REGION + wave * 64 * ROWB);
+    S.wdst = stage + wofs;
+    S.adst = stage + A_REGION + wofs;
     return S;
 }
 
 template <int EPI>
-__device__ __forceinline__ void issue_stage(uint32_t stage, const Cursor& I, int wave) {
-    const StageIssue S = stage_issue<EPI>(stage, I, wave);
+__device__ __forceinline__ void issue_stage(uint32_t stage, const Cursor& I, uint32_t wofs) {
+    const StageIssue S = stage_issue<EPI>(stage, I, wofs);
 #pragma unroll
     for (int i = 0; i < 16; ++i) issue_one<EPI>(S, I.L, i);
 }
@@ -349,18 +363,15 @@ __device__ __forceinline__ void issue_stage(uint32_t stage, const Cursor& I, int
 // The scales of the cursor's tile when its k-step starts the tile: wave w loads sa of token rows 64 w .. 64 w + 63
 // and sb of weight rows 64 w .. 64 w + 63 into scale set c % NSCALE (a scalar scale has stride 0 and fills every
 // entry).  At any other k-step the two loads read nothing and land in the scratch slot.
-__device__ __forceinline__ void issue_scales(uint32_t lds0, const Cursor& I, int wave) {
+__device__ __forceinline__ void issue_scales(uint32_t lds0, const Cursor& I) {
     const bool real = I.valid && I.ks == 0;
-    const uint32_t base = lds0 + SCALES_OFF + (uint32_t)(I.c % NSCALE) * SCALE_SET;
-    const uint32_t dsa = __builtin_amdgcn_readfirstlane(real ? base + 256 * wave : lds0 + JUNK_OFF);
-    const uint32_t dsb = __builtin_amdgcn_readfirstlane(real ? base + 1024 + 256 * wave : lds0 + JUNK_OFF + 256);
-    dma4(I.L.rsa, dsa, real ? I.L.sa_off : OOB);
-    dma4(I.L.rsb, dsb, real ? I.L.sb_off : OOB);
+    dma4(I.L.rsa, real ? I.dsa : lds0 + JUNK_OFF, real ? I.L.sa_off : OOB);
+    dma4(I.L.rsb, real ? I.dsb : lds0 + JUNK_OFF + 256, real ? I.L.sb_off : OOB);
 }
 
 template <int EPI, bool GROUPED>
-__device__ __forceinline__ void cursor_next(Cursor& I, const GroupedParams& gp, int wave, int lane) {
-    if (++I.ks == I.nk) cursor_set<EPI, GROUPED>(I, gp, I.c + 1, wave, lane);
+__device__ __forceinline__ void cursor_next(Cursor& I, const GroupedParams& gp, uint32_t lds0, int wave, int lane) {
+    if (++I.ks == I.nk) cursor_set<EPI, GROUPED>(I, gp, I.c + 1, lds0, wave, lane);
 }
 
 // One k-step g (stage g & 1 holds it, its sub-step-0 fragments are in fa0/fb0, the loads of k-step g+1 are in flight;
@@ -389,11 +400,11 @@ constexpr int ks_loads_before_pub() {
 }
 
 template <int EPI, bool READ_NEXT>
-__device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, int wave, int wn, int wm,
+__device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, uint32_t wofs, int wn, int wm,
                                       int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4], v8i fb1[4]) {
     uint8_t* cur = lds + (g & 1) * STAGE_BYTES;
     uint8_t* nxt = lds + ((g + 1) & 1) * STAGE_BYTES;
-    const StageIssue S = stage_issue<EPI>(lds0 + (uint32_t)(g & 1) * STAGE_BYTES, I, wave);
+    const StageIssue S = stage_issue<EPI>(lds0 + (uint32_t)(g & 1) * STAGE_BYTES, I, wofs);
     constexpr int NREAD = 31 - KS_PUB;                  // MFMAs that carry the next k-step's reads
     constexpr int PER = (8 + NREAD - 1) / NREAD;
 #pragma unroll
@@ -406,7 +417,7 @@ __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const 
             barrier_nofence();                          // ... and every wave's: the stage is free
         }
         if (u > KS_REL && u <= KS_REL + 16) issue_one<EPI>(S, I.L, u - KS_REL - 1);
-        if (u == KS_REL + 9) issue_scales(lds0, I, wave);
+        if (u == KS_REL + 9) issue_scales(lds0, I);
         if (u == KS_PUB) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(ks_loads_before_pub()));   // k-step g+1 (and older) has landed
             barrier_nofence();
@@ -474,27 +485,23 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
     };
     // the wave reads back its own staging tile (LDS accesses of one wave complete in order): 16 bytes per lane, 8
     // lanes per 128-byte row segment, 8 rows per store instruction
-    uint16_t* ybase = reinterpret_cast<uint16_t*>(p.y);
+    // Stores go through a buffer descriptor whose range ends at the last valid element: rows at or past M fall out of
+    // range and are dropped by the hardware, columns at or past the output width get an out-of-range offset.  No
+    // branch: partial tiles take the same instruction stream as whole ones.
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(p.y, p.y_bytes);
+    const uint32_t row2 = (uint32_t)p.ldy * 2u;         // bytes per output row
     auto flush = [&](int m0, int col0, int ncols) {
         const int c = lane & 7;
         const int col = col0 + c * 8;
-        uint4 v[4];
+        v4u v[4];
 #pragma unroll
         for (int it = 0; it < 4; ++it) {                // all four reads before the first store
             const int ml = it * 8 + (lane >> 3);
-            v[it] = *reinterpret_cast<const uint4*>(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+            v[it] = *reinterpret_cast<const v4u*>(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
         }
-        uint16_t* yrow = ybase + (int64_t)(m0 + (lane >> 3)) * p.ldy + col;
-        if (m0 + 32 <= p.M && col0 + 64 <= ncols) {     // whole 32 x 64 piece in range (uniform): no per-row test
+        const uint32_t off = (col < ncols) ? (uint32_t)(m0 + (lane >> 3)) * row2 + (uint32_t)col * 2u : OOB;
 #pragma unroll
-            for (int it = 0; it < 4; ++it) *reinterpret_cast<uint4*>(yrow + (int64_t)(it * 8) * p.ldy) = v[it];
-        } else {
-#pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                const int m = m0 + it * 8 + (lane >> 3);
-                if (m < p.M && col < ncols) *reinterpret_cast<uint4*>(yrow + (int64_t)(it * 8) * p.ldy) = v[it];
-            }
-        }
+        for (int it = 0; it < 4; ++it) __builtin_amdgcn_raw_buffer_store_b128(v[it], yr, off + (uint32_t)it * 8u * row2, 0, 0);
     };
     auto row_amax = [&](uint32_t v, int m) {
         const uint32_t o = (uint32_t)__shfl_xor((int)v, 32, 64);
@@ -529,11 +536,12 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                 for (int q = 0; q < 4; ++q) {
                     const int f = col0 + 32 * t + 8 * q + 4 * hi;
                     float bg[4] = {0, 0, 0, 0}, bu[4] = {0, 0, 0, 0};
-                    if (HAS_BIAS && f < F) {
+                    if (HAS_BIAS) {                     // columns past F read column 0 (not stored)
+                        const int fc = f < F ? f : 0;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            bg[r] = load_bias(p.bias, f + r, 0);
-                            bu[r] = load_bias(p.bias, F + f + r, 0);
+                            bg[r] = load_bias(p.bias, fc + r, 0);
+                            bu[r] = load_bias(p.bias, F + fc + r, 0);
                         }
                     }
 #pragma unroll
@@ -600,9 +608,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                         const bool ok = n < p.N && m < p.M;
                         const v4f sbn = sb_v[i][q];
                         float bn[4] = {0, 0, 0, 0};
-                        if (HAS_BIAS && n < p.N) {
+                        if (HAS_BIAS) {                 // columns past N read column 0 (not stored)
+                            const int nc = n < p.N ? n : 0;
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) bn[r] = load_bias(p.bias, n + r, OUT_DT);
+                            for (int r = 0; r < 4; ++r) bn[r] = load_bias(p.bias, nc + r, OUT_DT);
                         }
                         float v[4];
 #pragma unroll
@@ -638,24 +647,25 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: LDS addresses go to SGPRs
     const int wn = wave & 1, wm = wave >> 1;
     const int G = (int)gridDim.x;
 
     Cursor I;
-    cursor_set<EPI, GROUPED>(I, gp, 0, wave, lane);
+    const uint32_t lds0 = lds_addr(lds);
+    const uint32_t wofs = (uint32_t)wave * 64u * ROWB;  // the wave's 64-row share of a stage region
+    cursor_set<EPI, GROUPED>(I, gp, 0, lds0, wave, lane);
     if (!I.valid) return;
 
     // prologue: k-steps 0 and 1 (and the scales of their tiles) in flight, the sub-step-0 fragments of k-step 0 in
     // registers; every load group is 16 stage loads followed by 2 scale loads
     v8i fa0[4], fb0[4], fa1[4], fb1[4];
-    const uint32_t lds0 = lds_addr(lds);
-    issue_stage<EPI>(lds0, I, wave);
-    issue_scales(lds0, I, wave);
-    cursor_next<EPI, GROUPED>(I, gp, wave, lane);
-    issue_stage<EPI>(lds0 + STAGE_BYTES, I, wave);
-    issue_scales(lds0, I, wave);
-    if (I.valid) cursor_next<EPI, GROUPED>(I, gp, wave, lane);
+    issue_stage<EPI>(lds0, I, wofs);
+    issue_scales(lds0, I);
+    cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
+    issue_stage<EPI>(lds0 + STAGE_BYTES, I, wofs);
+    issue_scales(lds0, I);
+    if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(18));
     barrier_nofence();
     read_frags<EPI>(lds, wn, wm, lane, 0, fa0, fb0);
@@ -677,15 +687,17 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
         for (int ks = 0; ks < nk - 1; ++ks, ++g) {
-            kstep<EPI, true>(lds, lds0, g, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-            if (I.valid) cursor_next<EPI, GROUPED>(I, gp, wave, lane);
+            kstep<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+            if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
         }
         // the tile's last k-step publishes the next k-step's stage but leaves its fragment registers free for the
         // epilogue; they are read after it
-        kstep<EPI, false>(lds, lds0, g, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-        if (I.valid) cursor_next<EPI, GROUPED>(I, gp, wave, lane);
+        kstep<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
         ++g;
         epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
+        // the next tile's fragment reads stay after the epilogue: hoisted into it they would hold 64 VGPRs across it
+        __builtin_amdgcn_sched_barrier(0);
         if (id + G >= gp.total_tiles) break;
         read_frags<EPI>(lds + (g & 1) * STAGE_BYTES, wn, wm, lane, 0, fa0, fb0);
     }
@@ -746,6 +758,7 @@ int check_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const flo
     H3_REQUIRE((w_rows - 1) * ldw + K <= kMaxBufferBytes, "%s: weight too large for one buffer range", who);
     H3_REQUIRE((w_rows - 1) * sb_stride * 4 + 4 <= kMaxBufferBytes, "%s: sb too large", who);
     H3_REQUIRE(lda * 512 <= kMaxBufferBytes, "%s: lda too large", who);
+    H3_REQUIRE(ldy * 4 * 512 <= kMaxBufferBytes, "%s: ldy too large", who);
     return H3FP8_OK;
 }
 
@@ -761,6 +774,7 @@ GemmParams make_params(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t 
     p.w_rows = (int)w_rows;
     p.a_bytes = (uint32_t)((M - 1) * lda + K);
     p.w_bytes = (uint32_t)((w_rows - 1) * ldw + K);
+    p.y_bytes = (uint32_t)(((M - 1) * ldy + N) * 2);   // bf16 / fp16 (the fp32 probe stores without the descriptor)
     const int64_t n_tile_cols = swiglu ? (BN / 2) : BN;
     p.tiles_m = (int)((M + BM - 1) / BM);
     p.tiles_n = (int)((N + n_tile_cols - 1) / n_tile_cols);
@@ -776,6 +790,8 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
              hipStream_t st) {
     int64_t rows_per = std::max<int64_t>(BM, ((kMaxBufferBytes - K) / lda + 1) / BM * BM);
     if (sa_stride > 0) rows_per = std::min<int64_t>(rows_per, std::max<int64_t>(BM, kMaxBufferBytes / (4 * sa_stride) / BM * BM));
+    // the output's byte offsets (stored through a range-checked descriptor) are 32-bit as well
+    rows_per = std::min<int64_t>(rows_per, std::max<int64_t>(BM, kMaxBufferBytes / (4 * ldy) / BM * BM));
     const int out_elem = (out_dt == H3FP8_DT_F32) ? 4 : 2;
     for (int64_t r0 = 0; r0 < M; r0 += rows_per) {
         const int64_t Mi = std::min<int64_t>(rows_per, M - r0);
@@ -874,6 +890,8 @@ int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream) {
         if (rc) return rc;
         H3_REQUIRE(g.M == 0 || (g.M - 1) * g.lda + g.K <= kMaxBufferBytes,
                    "h3fp8_grouped_gemm: group %d activation too large for one launch", i);
+        H3_REQUIRE(g.M == 0 || ((g.M - 1) * g.ldy + g.N) * 2 <= kMaxBufferBytes,
+                   "h3fp8_grouped_gemm: group %d output too large for one launch", i);
         H3_REQUIRE(g.M == 0 || (g.M - 1) * g.sa_stride * 4 + 4 <= kMaxBufferBytes,
                    "h3fp8_grouped_gemm: group %d scales too large for one launch", i);
         if (g.M == 0 || g.N == 0) continue;
