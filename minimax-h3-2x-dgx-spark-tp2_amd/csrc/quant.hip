@@ -32,14 +32,23 @@ __device__ __forceinline__ uint32_t chunk_absmax(uint4 v) {
     return m;
 }
 
+// x * inv clamped to [-448, 448].  FINITE: the row maximum is finite, so x * inv is finite and a median-of-three is the
+// clamp exactly (one instruction); otherwise the reference's compare/select clamp, which keeps NaN.
+template <bool FINITE>
+__device__ __forceinline__ float scaled_clamp(float x, float inv) {
+    if (FINITE) return __builtin_amdgcn_fmed3f(x * inv, -H3_FP8_MAX, H3_FP8_MAX);
+    return quant_clamp(x, inv);
+}
+
 // 8 bf16 -> 8 e4m3fn bytes with the given inverse scale.
+template <bool FINITE>
 __device__ __forceinline__ uint2 chunk_quant(uint4 v, float inv) {
     uint32_t w[4] = {v.x, v.y, v.z, v.w};
     float f[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        f[2 * i] = quant_clamp(u2f(w[i] << 16), inv);
-        f[2 * i + 1] = quant_clamp(u2f(w[i] & 0xffff0000u), inv);
+        f[2 * i] = scaled_clamp<FINITE>(u2f(w[i] << 16), inv);
+        f[2 * i + 1] = scaled_clamp<FINITE>(u2f(w[i] & 0xffff0000u), inv);
     }
     return make_uint2(e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7]));
 }
@@ -79,10 +88,18 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restr
     const float s = row_scale(amax);
     const float inv = inv_scale(s);
     uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
+    if (__builtin_amdgcn_readfirstlane(f2u(amax) & 0x7fffffffu) < 0x7f800000u) {   // wave-uniform: finite maximum
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        int64_t c = lane + 64 * j;
-        if (c < nchunk) qr[c] = chunk_quant(v[j], inv);
+        for (int j = 0; j < CPL; ++j) {
+            int64_t c = lane + 64 * j;
+            if (c < nchunk) qr[c] = chunk_quant<true>(v[j], inv);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            int64_t c = lane + 64 * j;
+            if (c < nchunk) qr[c] = chunk_quant<false>(v[j], inv);
+        }
     }
     if (lane == 0) scale[row] = s;
 }
@@ -112,7 +129,7 @@ __global__ void __launch_bounds__(256) quant_rows_wide_kernel(const uint16_t* __
     const float s = row_scale(amax);
     const float inv = inv_scale(s);
     uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
-    for (int64_t c = lane; c < nchunk; c += 64) qr[c] = chunk_quant(xr[c], inv);
+    for (int64_t c = lane; c < nchunk; c += 64) qr[c] = chunk_quant<false>(xr[c], inv);
     if (lane == 0) scale[row] = s;
 }
 

@@ -10,6 +10,8 @@
 // The row-quant forms run one 256-thread workgroup per row: each thread owns CPT groups of 4 consecutive columns
 // (group c = tid + 256 j), keeps its bf16 h values in registers, and the row maximum is a wave xor-shuffle max plus a
 // 4-entry LDS exchange; the quant then reuses the registers (the row is read from HBM once).
+#include <algorithm>
+
 #include "h3fp8_common.h"
 
 namespace {
@@ -63,6 +65,16 @@ __device__ __forceinline__ void swiglu_group(const void* __restrict__ x, int64_t
         h[2] = swiglu_bits(gw.y & 0xffffu, uw.y & 0xffffu, silu);
         h[3] = swiglu_bits(gw.y >> 16, uw.y >> 16, silu);
     }
+}
+
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+// max(m, |lo half|, |hi half|) of a packed bf16 pair, as fp32 bit patterns (NaN patterns order above +inf).
+__device__ __forceinline__ uint32_t max_abs_bf16x2_bits(uint32_t m, uint32_t p) {
+    const uint32_t lo = (p << 16) & 0x7fff0000u, hi = p & 0x7fff0000u;
+    m = m > lo ? m : lo;
+    return m > hi ? m : hi;
 }
 
 __device__ __forceinline__ uint32_t quant4(const uint32_t h[4], float inv) {
@@ -135,6 +147,96 @@ __global__ void __launch_bounds__(256) swiglu_quant_rows_kernel(const void* __re
     }
 }
 
+// bf16 [gate | up] -> e4m3 q + per-row scale, the HBM-bound form (fp8_quant_fuse.py:262-278): a persistent kernel with
+// the SiLU table in LDS (one 128 KiB copy per CU, loaded once), so the 65536-entry lookups are LDS gathers instead of
+// scattered global loads.  One 64-lane wave per row, rows wave_id, wave_id + waves, ...: lane l owns the 16-byte column
+// chunks l + 64 j of the gate and of the up half (coalesced 1 KiB per load instruction), the row's h values stay in
+// VGPRs as packed bf16 pairs, the row maximum is a wave xor-shuffle max (no LDS exchange, no barrier), and every q
+// store writes 8 bytes per lane, 512 contiguous bytes per instruction.
+constexpr int SMQ_WAVES = 8;                   // waves per workgroup (2 per SIMD; 3 measured slower)
+// Quant of one packed bf16 pair: e4m3 bytes of clamp(h * inv, -448, 448).  FINITE: the row maximum is finite, so every
+// h * inv is finite and a median-of-three is the clamp exactly; otherwise compare/select, which keeps NaN (the
+// reference's clamp, fp8_quant_fuse.py:105-111).
+template <bool FINITE>
+__device__ __forceinline__ float clamp448(float y) {
+    if (FINITE) return __builtin_amdgcn_fmed3f(y, -H3_FP8_MAX, H3_FP8_MAX);
+    y = (y < -H3_FP8_MAX) ? -H3_FP8_MAX : y;
+    return (y > H3_FP8_MAX) ? H3_FP8_MAX : y;
+}
+
+template <bool FINITE>
+__device__ __forceinline__ uint32_t quant_pairs(uint32_t p0, uint32_t p1, float inv) {
+    return e4m3x4(clamp448<FINITE>(u2f(p0 << 16) * inv), clamp448<FINITE>(u2f(p0 & 0xffff0000u) * inv),
+                  clamp448<FINITE>(u2f(p1 << 16) * inv), clamp448<FINITE>(u2f(p1 & 0xffff0000u) * inv));
+}
+
+template <int CPL, bool FINITE>
+__device__ __forceinline__ void store_q_row(const uint32_t (*h)[4], float inv, __amdgpu_buffer_rsrc_t qr, int lane) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const uint32_t lo = quant_pairs<FINITE>(h[j][0], h[j][1], inv);
+        const uint32_t hi = quant_pairs<FINITE>(h[j][2], h[j][3], inv);
+        const v2u v = {lo, hi};
+        // chunks past F fall outside the row's range and are dropped
+        __builtin_amdgcn_raw_buffer_store_b64(v, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
+    }
+}
+
+template <int CPL>
+__global__ void __launch_bounds__(64 * SMQ_WAVES) silu_mul_quant_lds_kernel(const uint16_t* __restrict__ x,
+                                                                          int64_t ldx, int64_t M, int64_t F,
+                                                                          const uint16_t* __restrict__ silu,
+                                                                          uint8_t* __restrict__ q, int64_t ldq,
+                                                                          float* __restrict__ scale) {
+    __shared__ __attribute__((aligned(16))) uint16_t tab[65536];
+    for (int i = threadIdx.x; i < 65536 / 8; i += 64 * SMQ_WAVES)
+        reinterpret_cast<v4u*>(tab)[i] = reinterpret_cast<const v4u*>(silu)[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * SMQ_WAVES;
+    float pz = 0.0f;
+    asm volatile("" : "+v"(pz));                        // an opaque +0 (the add below must not be folded away)
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: row addresses in SGPRs
+    for (int64_t m = (int64_t)blockIdx.x * SMQ_WAVES + wv; m < M; m += waves) {
+        // per-row buffer ranges: loads past F read zeros, stores past F are dropped (no per-chunk branch)
+        const __amdgpu_buffer_rsrc_t gr = make_rsrc(x + m * ldx, (uint32_t)(2 * F));
+        const __amdgpu_buffer_rsrc_t ur = make_rsrc(x + m * ldx + F, (uint32_t)(2 * F));
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + m * ldq, (uint32_t)F);
+        v4u gv[CPL], uv[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t off = (uint32_t)(lane + 64 * j) * 16u;
+            gv[j] = __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 2);   // aux 2: streaming (nt)
+            uv[j] = __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, 2);
+        }
+        uint32_t h[CPL][4];                             // packed bf16 h pairs
+        u16x2_t mx2 = {0, 0};                           // two running maxima of |h| bit patterns
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t g2 = gv[j][k], u2 = uv[j][k];
+                // u + (+0): -0 up becomes +0 under round-to-nearest, every other value (NaN included) is unchanged
+                // (fp8_swiglu.py:66)
+                const float u0 = bf16_to_f32(u2 & 0xffffu) + pz, u1 = u2f(u2 & 0xffff0000u) + pz;
+                const float s0 = bf16_to_f32(tab[g2 & 0xffffu]), s1 = bf16_to_f32(tab[g2 >> 16]);
+                const uint32_t hp = cvt_bf16x2(s0 * u0, s1 * u1);   // s * u exact in fp32, one RNE to bf16
+                h[j][k] = hp;
+                // columns past F read zeros (h = +0) and leave the maximum unchanged; |h| bit patterns order like
+                // |h| with NaN above +inf, so an unsigned 16-bit max per half is the NaN-propagating row maximum
+                mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2_t, hp & 0x7fff7fffu));
+            }
+        }
+        uint32_t mx = mx2[0] > mx2[1] ? (uint32_t)mx2[0] : (uint32_t)mx2[1];
+        mx = wave_max_u32(mx << 16);
+        const float s = row_scale(u2f(mx));
+        const float inv = inv_scale(s);
+        if (mx < 0x7f800000u) store_q_row<CPL, true>(h, inv, qr, lane);    // wave-uniform: finite row maximum
+        else store_q_row<CPL, false>(h, inv, qr, lane);
+        if (lane == 0) scale[m] = s;
+    }
+}
+
 // fp32 product -> bf16 h, elementwise: one thread per group of 4 columns.
 __global__ void __launch_bounds__(256) scale_swiglu_kernel(const float* __restrict__ x, int64_t ldx, int64_t M,
                                                            int64_t F, EpiArgs e, const uint16_t* __restrict__ silu,
@@ -171,6 +273,28 @@ __global__ void __launch_bounds__(256) scale_bias_cast_kernel(const float* __res
     *reinterpret_cast<uint2*>(y + m * ldy + n) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
 }
 
+// The persistent LDS-table form of the bf16-source pass, when its 16-byte loads and 8-byte stores are aligned and a row
+// fits in registers (F <= 8192); returns false to take the one-workgroup-per-row kernel instead.
+bool launch_silu_mul_quant_lds(const void* x, int64_t ldx, int64_t M, int64_t F, const uint16_t* silu, void* q,
+                               int64_t ldq, float* scale, hipStream_t st) {
+    const int64_t cpl = ((F >> 3) + 63) / 64;
+    if (F % 8 != 0 || ldx % 8 != 0 || ldq % 8 != 0 || ((uintptr_t)q & 7) != 0 || cpl > 16) return false;
+    // buffer descriptors need 4-byte aligned bases: every row start is (16-byte x, 8-byte q, even strides)
+    const int64_t wgs = std::min<int64_t>((M + SMQ_WAVES - 1) / SMQ_WAVES, h3host::cu_count());
+    dim3 grid((unsigned)std::max<int64_t>(1, wgs)), block(64 * SMQ_WAVES);
+    const uint16_t* xp = (const uint16_t*)x;
+    uint8_t* qp = (uint8_t*)q;
+#define H3_L(N) hipLaunchKernelGGL((silu_mul_quant_lds_kernel<N>), grid, block, 0, st, xp, ldx, M, F, silu, qp, ldq, scale)
+    if (cpl <= 1) H3_L(1);
+    else if (cpl <= 2) H3_L(2);
+    else if (cpl <= 4) H3_L(4);
+    else if (cpl <= 8) H3_L(8);
+    else if (cpl <= 12) H3_L(12);
+    else H3_L(16);
+#undef H3_L
+    return true;
+}
+
 template <bool SRC_FP32>
 int launch_swiglu_quant(const void* x, int64_t ldx, int64_t M, int64_t F, const EpiArgs& e, void* q, int64_t ldq,
                         float* scale, hipStream_t st) {
@@ -178,6 +302,10 @@ int launch_swiglu_quant(const void* x, int64_t ldx, int64_t M, int64_t F, const 
     int rc = h3host::ensure_device_init();
     if (rc) return rc;
     const uint16_t* silu = h3host::silu_table_ptr();
+    if (!SRC_FP32 && launch_silu_mul_quant_lds(x, ldx, M, F, silu, q, ldq, scale, st)) {
+        H3_CHECK_HIP(hipGetLastError());
+        return H3FP8_OK;
+    }
     const int64_t cpt = ((F >> 2) + 255) / 256;
     dim3 grid((unsigned)M), block(256);
     uint8_t* qp = (uint8_t*)q;

@@ -72,6 +72,26 @@ def test_silu_mul_quant(cuda, M, F):
     assert_quant_equal(q, s, *O.quant_rows(hh))
 
 
+# Shapes of the persistent LDS-table form (F <= 8192, F % 8 == 0): ragged 16-byte chunk counts per lane (F = 1000,
+# 520, 8184), one workgroup with idle waves (M = 3), several rows per wave (M = 4500 over at most 2048 waves), and a
+# strided input (a row stride past 2F).
+@pytest.mark.parametrize("M,F,pad", [(3, 1000, 0), (4500, 520, 0), (2600, 8192, 0), (77, 8184, 0), (300, 4096, 24)])
+def test_silu_mul_quant_persistent_form(cuda, M, F, pad):
+    from h3_tp2_amd import ops
+    g = torch.Generator().manual_seed(M * 7 + F)
+    base = (torch.randn(M, 2 * F + pad, generator=g) * 4).to(torch.bfloat16)
+    base[:, :7] = torch.tensor([0.0, -0.0, 1e-38, -88.0, 88.0, 3.0, -3.0]).to(torch.bfloat16)
+    base[:, F:F + 7] = torch.tensor([-0.0, 0.0, -0.0, 1.0, -1.0, -0.0, 0.0]).to(torch.bfloat16)
+    if M > 2:
+        base[1, 5] = float("nan")            # NaN gate: NaN h, NaN row maximum
+        base[2, F + 3] = float("inf")        # inf up: inf h in row 2
+    x = base[:, :2 * F]
+    q, s = ops.silu_mul_quant(base.to(cuda)[:, :2 * F])
+    torch.cuda.synchronize()
+    hh = O.swiglu_bf16(bits16(x.contiguous()))
+    assert_quant_equal(q, s, *O.quant_rows(hh))
+
+
 @pytest.mark.parametrize("M,F,K", [(200, 320, 512), (333, 1024, 1024), (257, 4096, 3072), (64, 8192, 256),
                                    (1, 128, 64)])
 @pytest.mark.parametrize("bias", [False, True])
