@@ -881,8 +881,6 @@ int h3fp8_gemm_swiglu_quant(const void* a, int64_t lda, const void* w_gate_up, i
 
 int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream) {
     H3_REQUIRE(groups && n_groups >= 0 && n_groups <= H3FP8_MAX_GROUPS, "h3fp8_grouped_gemm: bad group list");
-    GroupedParams gp{};
-    int tiles = 0;
     for (int i = 0; i < n_groups; ++i) {
         const h3fp8_group& g = groups[i];
         int rc = check_gemm(g.a, g.lda, g.w, g.ldw, g.sa, g.sa_stride, g.sb, g.sb_stride, g.y, g.ldy, g.M, g.N, g.K,
@@ -894,6 +892,17 @@ int h3fp8_grouped_gemm(const h3fp8_group* groups, int n_groups, void* stream) {
                    "h3fp8_grouped_gemm: group %d output too large for one launch", i);
         H3_REQUIRE(g.M == 0 || (g.M - 1) * g.sa_stride * 4 + 4 <= kMaxBufferBytes,
                    "h3fp8_grouped_gemm: group %d scales too large for one launch", i);
+    }
+    // A tile costs ceil(K / 128) k-steps whatever its M and N, and workgroup b takes tiles b, b + G, ...: with the
+    // groups' tile ranges in descending order of K, the last rounds are filled with the cheapest tiles (longest
+    // processing time first), so the workgroups finish close together.
+    int order[H3FP8_MAX_GROUPS];
+    for (int i = 0; i < n_groups; ++i) order[i] = i;
+    std::stable_sort(order, order + n_groups, [&](int x, int y) { return groups[x].K > groups[y].K; });
+    GroupedParams gp{};
+    int tiles = 0;
+    for (int k = 0; k < n_groups; ++k) {
+        const h3fp8_group& g = groups[order[k]];
         if (g.M == 0 || g.N == 0) continue;
         GemmParams p = make_params((const uint8_t*)g.a, g.lda, (const uint8_t*)g.w, g.ldw, g.sa, g.sa_stride, g.sb,
                                    g.sb_stride, nullptr, g.y, g.ldy, g.M, g.N, g.K, g.N, nullptr, nullptr, false);
