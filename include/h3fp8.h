@@ -128,6 +128,34 @@ int h3fp8_silu_mul_quant(const void* x, int64_t ldx, int64_t M, int64_t F, void*
                          void* stream);
 
 /*
+ * The per-token quant fused into its producers (one wavefront per row, H % 8 == 0, H <= 8192):
+ *   h3fp8_rms_quant       rms_norm_indexed_scale_shift + quant: the qkv site's producer.  Replaces the reference's
+ *                         rms_quant / _rms_norm_indexed_scale_shift_quant_kernel (h3_tp2/fp8_quant_fuse.py:330-346,
+ *                         :143-188).
+ *   h3fp8_gate_rms_quant  indexed_gate_rms_norm_scale_shift + quant: the fc1 site's producer; also writes residual_out.
+ *                         Replaces gate_rms_quant / _indexed_gate_rms_norm_scale_shift_quant_kernel
+ *                         (h3_tp2/fp8_quant_fuse.py:349-369, :191-243).
+ * Per row m, i = indices[m * idx_stride] (int32 if idx_bytes == 4, int64 if 8):
+ *   [gate form] u = bf16(residual + gate[i] * branch) -> residual_out[m]; x = u
+ *   var = fp32(sum_k x_k^2) / H; r = 1 / sqrt(var + eps)
+ *   h = bf16(((x * r) * weight) * (1 + scale[i]) + shift[i]), every fp32 operation rounded on its own
+ *   q [M, H] e4m3fn, qscale [M]: h3fp8_quant_rows of h; with h_out != NULL h is stored there too (bf16 [M, H]).
+ * gate / shift / scale are [n_index, H] bf16 tables with row strides ld_gate / ld_shift / ld_scale (the chunk views
+ * of an AdaLN modulation tensor); every bf16 row is 16-byte aligned with a stride that is a multiple of 8 elements.
+ * The sum of squares is taken in fp64 and rounded once (exact for rows whose squares span < ~40 binades).  An index
+ * outside [0, n_index) is not read through: that row's residual_out, h and codes are NaN and its scale NaN.
+ */
+int h3fp8_rms_quant(const void* x, int64_t ldx, const void* weight, const void* shift, int64_t ld_shift,
+                    const void* scale, int64_t ld_scale, int64_t n_index, const void* indices, int64_t idx_stride,
+                    int idx_bytes, int64_t M, int64_t H, float eps, void* q, int64_t ldq, float* qscale, void* h_out,
+                    int64_t ldh, void* stream);
+int h3fp8_gate_rms_quant(const void* residual, int64_t ldr, const void* gate, int64_t ld_gate, const void* branch,
+                         int64_t ld_branch, const void* weight, const void* shift, int64_t ld_shift, const void* scale,
+                         int64_t ld_scale, int64_t n_index, const void* indices, int64_t idx_stride, int idx_bytes,
+                         int64_t M, int64_t H, float eps, void* residual_out, int64_t ld_res, void* q, int64_t ldq,
+                         float* qscale, void* h_out, int64_t ldh, void* stream);
+
+/*
  * The two-pass scale pass: y = round(sa[m] * (sb[n] * x32[m, n])) (bias: one fma), bf16 or fp16.
  * Replaces fp8_gemm._scale_bias_cast / _launch (h3_tp2/fp8_gemm.py:37-54, :167-171) and the consumers' stash
  * materialisation (h3_tp2/fp8_consumers.py:373-380).

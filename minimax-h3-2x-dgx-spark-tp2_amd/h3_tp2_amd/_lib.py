@@ -45,6 +45,10 @@ _SIGS = {
     "h3fp8_scale_swiglu": ([P, I64, P, I64, P, I64, P, I64, I64, P, I64, P], I),
     "h3fp8_scale_swiglu_quant": ([P, I64, P, I64, P, I64, P, I64, I64, P, I64, P, P], I),
     "h3fp8_silu_mul_quant": ([P, I64, I64, I64, P, I64, P, P], I),
+    "h3fp8_rms_quant": ([P, I64, P, P, I64, P, I64, I64, P, I64, I, I64, I64, ctypes.c_float, P, I64, P, P, I64, P],
+                        I),
+    "h3fp8_gate_rms_quant": ([P, I64, P, I64, P, I64, P, P, I64, P, I64, I64, P, I64, I, I64, I64, ctypes.c_float,
+                              P, I64, P, I64, P, P, I64, P], I),
     "h3fp8_scale_bias_cast": ([P, I64, P, I64, P, I64, P, P, I64, I, I64, I64, P], I),
     "h3fp8_grouped_gemm": ([ctypes.POINTER(Group), I, P], I),
     "h3fp8_selfcheck_e4m3": ([ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], I),

@@ -226,6 +226,67 @@ def silu_mul_quant(x: torch.Tensor):
     return q, s
 
 
+# ---- the quant fused into its producers --------------------------------------------------------------------------
+
+def _producer_args(x: torch.Tensor, weight: torch.Tensor, tables: tuple, indices: torch.Tensor, names: tuple):
+    """Checks shared by the two producers: bf16 rows, weight [H], [B, H] tables, indices int32/int64 [M]."""
+    _need_cuda(x, weight, indices, *tables)
+    M, H = x.shape
+    for t, n in ((x, "x"), *zip(tables, names)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{n} must be bfloat16, got {t.dtype}")
+        _rows(t, n)
+    if weight.dtype != torch.bfloat16 or weight.numel() != H or (H > 1 and weight.reshape(-1).stride(0) != 1):
+        raise ValueError(f"weight must be a contiguous bfloat16 [{H}] vector")
+    n_index = min(t.shape[0] for t in tables)
+    if any(t.shape[1] != H for t in tables):
+        raise ValueError(f"{', '.join(names)} must have {H} columns")
+    if indices.dim() != 1 or indices.shape[0] != M or indices.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"indices must be int32/int64 [{M}], got {indices.dtype} {tuple(indices.shape)}")
+    return M, H, n_index, indices.element_size()
+
+
+def _placeholder(ph: torch.Tensor | None, like: torch.Tensor) -> tuple[int | None, int]:
+    if ph is None:
+        return None, 0
+    if ph.shape != like.shape or ph.dtype != torch.bfloat16 or ph.device != like.device:
+        raise ValueError(f"ph must be bfloat16 {tuple(like.shape)} on {like.device}")
+    return ph.data_ptr(), _rows(ph, "ph")
+
+
+def rms_quant(x: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+              indices: torch.Tensor, eps: float, ph: torch.Tensor | None = None):
+    """``rms_norm_indexed_scale_shift`` + the per-token quant of its output: (fp8 [M, H], scale [M, 1]); with ``ph``
+    (bf16 [M, H]) the modulated bf16 row is stored there too (h3_tp2/fp8_quant_fuse.py:330-346)."""
+    M, H, n_index, ib = _producer_args(x, weight, (shift, scale), indices, ("shift", "scale"))
+    q = torch.empty((M, H), device=x.device, dtype=E4M3)
+    s = torch.empty((M, 1), device=x.device, dtype=torch.float32)
+    _lib.call("h3fp8_rms_quant", x.data_ptr(), _rows(x, "x"), weight.data_ptr(), shift.data_ptr(),
+              _rows(shift, "shift"), scale.data_ptr(), _rows(scale, "scale"), n_index, indices.data_ptr(),
+              indices.stride(0), ib, M, H, float(eps), q.data_ptr(), H, s.data_ptr(), *_placeholder(ph, x), _stream(x))
+    return q, s
+
+
+def gate_rms_quant(residual: torch.Tensor, gate: torch.Tensor, branch: torch.Tensor, weight: torch.Tensor,
+                   shift: torch.Tensor, scale: torch.Tensor, indices: torch.Tensor, eps: float,
+                   ph: torch.Tensor | None = None):
+    """``indexed_gate_rms_norm_scale_shift`` with the modulated output quantised per token: (residual_out bf16 [M, H],
+    fp8 [M, H], scale [M, 1]); ``ph`` as in ``rms_quant`` (h3_tp2/fp8_quant_fuse.py:349-369)."""
+    M, H, n_index, ib = _producer_args(residual, weight, (gate, shift, scale), indices, ("gate", "shift", "scale"))
+    if branch.shape != residual.shape or branch.dtype != torch.bfloat16:
+        raise ValueError("branch must be bfloat16 with the residual's shape")
+    _need_cuda(branch)
+    res = torch.empty((M, H), device=residual.device, dtype=torch.bfloat16)
+    q = torch.empty((M, H), device=residual.device, dtype=E4M3)
+    s = torch.empty((M, 1), device=residual.device, dtype=torch.float32)
+    _lib.call("h3fp8_gate_rms_quant", residual.data_ptr(), _rows(residual, "residual"), gate.data_ptr(),
+              _rows(gate, "gate"), branch.data_ptr(), _rows(branch, "branch"), weight.data_ptr(), shift.data_ptr(),
+              _rows(shift, "shift"), scale.data_ptr(), _rows(scale, "scale"), n_index, indices.data_ptr(),
+              indices.stride(0), ib, M, H, float(eps), res.data_ptr(), H, q.data_ptr(), H, s.data_ptr(),
+              *_placeholder(ph, residual), _stream(residual))
+    return res, q, s
+
+
 def scale_bias_cast(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
                     out_dtype: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:
     """The two-pass scale pass: round(sa * (sb * x32)) (+ bias by one fma) (h3_tp2/fp8_gemm.py:37-54, :167-171)."""

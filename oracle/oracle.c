@@ -244,3 +244,101 @@ void oracle_bf16_rne_array(const float* x, int64_t n, uint16_t* out) {
 void oracle_fp16_rne_array(const float* x, int64_t n, uint16_t* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = oracle_fp16_rne(x[i]);
 }
+
+/* ---- producers with the quant fused in (h3_tp2/fp8_quant_fuse.py:143-243, :330-369) -------------------------------
+ *
+ * The stock producers, as the reference's CPU stand-ins state them (tests/fake_h3_consumers.py:66-84):
+ *   gate form:  u = bf16(residual + gate[i] * branch)                      (fp32 multiply, fp32 add, one rounding)
+ *   var = fp32(sum_k x_k * x_k) / H;  r = 1 / sqrt(var + eps)              (torch's CPU rsqrt is 1 / sqrt)
+ *   h_k = bf16(((x_k * r) * weight_k) * (1 + scale[i]_k) + shift[i]_k)     (each operation rounded on its own)
+ * followed by quant_rows of h.
+ *
+ * The sum of squares: each x_k * x_k is an fp32 product (exact unless it falls below the normal range), the products
+ * are added in fp64 in a fixed order and the total is rounded once to fp32.  For rows whose squares span fewer than
+ * about 40 binades the fp64 sum is exact, so the order does not matter and fp32(sum) is the correctly rounded sum the
+ * stock kernel's fp32 reduction approximates.  The order fixed here is the HIP kernel's: 64 partial sums, partial l
+ * over the 16-byte chunks c = l, l + 64, l + 128, ... of the row (8 elements each, ascending), then an xor butterfly
+ * over the partials with distances 32, 16, ..., 1 (p_l <- p_l + p_(l xor d)). */
+double oracle_row_sumsq(const float* x, int64_t H) {
+    double p[64];
+    const int64_t nchunk = H / 8;
+    for (int l = 0; l < 64; ++l) {
+        double s = 0.0;
+        for (int64_t c = l; c < nchunk; c += 64)
+            for (int e = 0; e < 8; ++e) {
+                const float v = x[8 * c + e];
+                s += (double)(v * v);
+            }
+        p[l] = s;
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        double t[64];
+        for (int l = 0; l < 64; ++l) t[l] = p[l] + p[l ^ d];
+        memcpy(p, t, sizeof(p));
+    }
+    return p[0];
+}
+
+/* One row: x (fp32 values of bf16), weight / shift / scale rows (bf16 bits) -> h (bf16 bits). */
+static void rms_mod_row(const float* x, int64_t H, const uint16_t* weight, const uint16_t* shift,
+                        const uint16_t* scale, float eps, uint16_t* h) {
+    volatile float var = (float)oracle_row_sumsq(x, H);
+    volatile float hf = (float)H;
+    var = var / hf;
+    volatile float t = var + eps;
+    volatile float d = sqrtf(t);
+    volatile float one = 1.0f;
+    const float r = one / d;
+    for (int64_t k = 0; k < H; ++k) {
+        volatile float n = x[k] * r;
+        n = n * oracle_bf16_to_f32(weight[k]);
+        volatile float g = 1.0f + oracle_bf16_to_f32(scale[k]);
+        volatile float o = n * g;
+        o = o + oracle_bf16_to_f32(shift[k]);
+        h[k] = oracle_bf16_rne(o);
+    }
+}
+
+/* rms_norm_indexed_scale_shift + quant (fp8_quant_fuse.py:143-188, :330-346).  x [M, H] bf16 (row stride ldx);
+ * weight [H]; shift / scale: row indices[m] of [B, H] tables (row strides ld_shift / ld_scale); indices int64 [M].
+ * Outputs: h [M, H] bf16 (row stride H, may be NULL), q [M, H] (row stride H), qscale [M]. */
+void oracle_rms_quant(const uint16_t* x, int64_t ldx, const uint16_t* weight, const uint16_t* shift, int64_t ld_shift,
+                      const uint16_t* scale, int64_t ld_scale, const int64_t* indices, int64_t M, int64_t H,
+                      float eps, uint16_t* h, uint8_t* q, float* qscale) {
+    float* xf = (float*)__builtin_alloca((size_t)H * 4);
+    uint16_t* hr = (uint16_t*)__builtin_alloca((size_t)H * 2);
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t i = indices[m];
+        for (int64_t k = 0; k < H; ++k) xf[k] = oracle_bf16_to_f32(x[m * ldx + k]);
+        rms_mod_row(xf, H, weight, shift + i * ld_shift, scale + i * ld_scale, eps, hr);
+        if (h) memcpy(h + m * H, hr, (size_t)H * 2);
+        for (int64_t k = 0; k < H; ++k) xf[k] = oracle_bf16_to_f32(hr[k]);
+        qscale[m] = oracle_quant_row_f32(xf, H, q + m * H);
+    }
+}
+
+/* indexed_gate_rms_norm_scale_shift + quant (fp8_quant_fuse.py:191-243, :349-369): residual_out [M, H] =
+ * bf16(residual + gate[i] * branch), then rms_quant's row on residual_out.  gate is a [B, H] table (row stride
+ * ld_gate) indexed like shift / scale; branch [M, H] (row stride ld_branch). */
+void oracle_gate_rms_quant(const uint16_t* residual, int64_t ldr, const uint16_t* gate, int64_t ld_gate,
+                           const uint16_t* branch, int64_t ld_branch, const uint16_t* weight, const uint16_t* shift,
+                           int64_t ld_shift, const uint16_t* scale, int64_t ld_scale, const int64_t* indices,
+                           int64_t M, int64_t H, float eps, uint16_t* residual_out, uint16_t* h, uint8_t* q,
+                           float* qscale) {
+    float* xf = (float*)__builtin_alloca((size_t)H * 4);
+    uint16_t* hr = (uint16_t*)__builtin_alloca((size_t)H * 2);
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t i = indices[m];
+        for (int64_t k = 0; k < H; ++k) {
+            volatile float p = oracle_bf16_to_f32(gate[i * ld_gate + k]) * oracle_bf16_to_f32(branch[m * ld_branch + k]);
+            volatile float u = oracle_bf16_to_f32(residual[m * ldr + k]) + p;
+            const uint16_t ub = oracle_bf16_rne(u);
+            residual_out[m * H + k] = ub;
+            xf[k] = oracle_bf16_to_f32(ub);
+        }
+        rms_mod_row(xf, H, weight, shift + i * ld_shift, scale + i * ld_scale, eps, hr);
+        if (h) memcpy(h + m * H, hr, (size_t)H * 2);
+        for (int64_t k = 0; k < H; ++k) xf[k] = oracle_bf16_to_f32(hr[k]);
+        qscale[m] = oracle_quant_row_f32(xf, H, q + m * H);
+    }
+}

@@ -16,13 +16,21 @@ Each function names the reference code it restates (paths relative to the refere
 * ``scale_swiglu_quant``  h3_tp2/fp8_swiglu.py:72-103
 * ``dequant_matmul``      h3_tp2/fp8_consumers.py:518-523 (``a.float() @ w.float().t()``, fp32); ``matmul_f32`` is the
                           same product through numpy's BLAS (any summation order) for large shapes.
+* ``rms_quant``           h3_tp2/fp8_quant_fuse.py:143-188, :330-346: the stock ``rms_norm_indexed_scale_shift`` as
+                          tests/fake_h3_consumers.py:77-84 states it, then ``quant_rows``
+* ``gate_rms_quant``      h3_tp2/fp8_quant_fuse.py:191-243, :349-369: ``indexed_gate_rms_norm_scale_shift``
+                          (tests/fake_h3_consumers.py:66-74), then ``quant_rows``
+* ``row_sumsq``           the sum of squares of those producers, in fp64, in the HIP kernel's fixed order
 
 Pinning (what each function is checked against, in tests/test_oracle.py): the e4m3fn/bf16/fp16 casts against torch's
 and numpy's own casts on exhaustive or dense sweeps; ``quant_rows`` against known answers of the reference's tests
 (zero row -> MIN_SCALE, every positive finite bf16 as a row maximum against IEEE division done by numpy), against the
 e4m3 grid (every code re-quantises to itself) and against brute-force nearest-grid search; ``epilogue`` against the
 order-sensitive known answer of tests/test_fp8_gemm.py:67-75 and against float64 arithmetic; ``silu_table`` against
-torch's CPU exp on all 65536 bf16 inputs and against float64; ``dequant_matmul`` against exact integer products.
+torch's CPU exp on all 65536 bf16 inputs and against float64; ``dequant_matmul`` against exact integer products;
+``row_sumsq`` against the exact sum (``math.fsum``); ``rms_quant`` / ``gate_rms_quant`` against closed forms
+(constant rows, power-of-two scale invariance), an index permutation, torch's CPU evaluation of the stand-ins (equal
+residual, modulated rows within one bf16 ulp) and their own composition with ``quant_rows``.
 """
 from __future__ import annotations
 
@@ -62,6 +70,11 @@ def lib() -> ctypes.CDLL:
         L.oracle_scale_swiglu.argtypes = [P, I64, I64, P, P, P, P]
         L.oracle_scale_swiglu_quant.argtypes = [P, I64, I64, P, P, P, P, P]
         L.oracle_dequant_matmul.argtypes = [P, I64, P, I64, I64, I64, I64, P]
+        L.oracle_row_sumsq.argtypes = [P, I64]
+        L.oracle_row_sumsq.restype = ctypes.c_double
+        F = ctypes.c_float
+        L.oracle_rms_quant.argtypes = [P, I64, P, P, I64, P, I64, P, I64, I64, F, P, P, P]
+        L.oracle_gate_rms_quant.argtypes = [P, I64, P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, F, P, P, P, P]
         L.oracle_e4m3fn_from_f32.argtypes = [ctypes.c_float]
         L.oracle_e4m3fn_from_f32.restype = ctypes.c_uint8
         L.oracle_bf16_rne.argtypes = [ctypes.c_float]
@@ -234,3 +247,57 @@ def linear(x_bf16_bits: np.ndarray, w_codes: np.ndarray, sb: np.ndarray, bias_bi
     """The whole reference CPU path of one online-FP8 linear: per-token quant of X, fp32 product, epilogue."""
     q, sa = quant_rows(x_bf16_bits)
     return epilogue(matmul_f32(q, w_codes), sa, sb, bias_bits, out_fp16), q, sa
+
+
+def row_sumsq(x_bf16_bits: np.ndarray) -> float:
+    """sum_k fp32(x_k * x_k) of one bf16 row (H % 8 == 0), in fp64, in the HIP kernel's fixed order."""
+    x = bf16_to_f32(_u16(x_bf16_bits).reshape(-1))
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return float(lib().oracle_row_sumsq(_p(x), x.size))
+
+
+def _table(t: np.ndarray) -> tuple[np.ndarray, int]:
+    """A [B, H] bf16 table (bit patterns, any row stride) -> (contiguous-row array, row stride in elements)."""
+    t = _u16(t)
+    return t, t.shape[1]
+
+
+def rms_quant(x_bits, weight_bits, shift_bits, scale_bits, indices, eps: float):
+    """bf16 x [M, H], weight [H], shift / scale [B, H] tables, indices [M] ->
+    (h bf16 bits [M, H], fp8 codes [M, H], fp32 scale [M])."""
+    x = _u16(x_bits)
+    M, H = x.shape
+    w = _u16(weight_bits).reshape(-1)
+    sh, ldsh = _table(shift_bits)
+    sc, ldsc = _table(scale_bits)
+    idx = np.ascontiguousarray(np.asarray(indices).reshape(-1), dtype=np.int64)
+    assert idx.size == M and w.size == H and sh.shape[1] == H and sc.shape[1] == H
+    assert M == 0 or (idx.min() >= 0 and idx.max() < min(sh.shape[0], sc.shape[0]))
+    h = np.empty((M, H), dtype=np.uint16)
+    q = np.empty((M, H), dtype=np.uint8)
+    s = np.empty((M,), dtype=np.float32)
+    lib().oracle_rms_quant(_p(x), H, _p(w), _p(sh), ldsh, _p(sc), ldsc, _p(idx), M, H, float(eps), _p(h), _p(q),
+                           _p(s))
+    return h, q, s
+
+
+def gate_rms_quant(residual_bits, gate_bits, branch_bits, weight_bits, shift_bits, scale_bits, indices, eps: float):
+    """bf16 residual / branch [M, H], gate / shift / scale [B, H] tables, weight [H], indices [M] ->
+    (residual_out bf16 bits [M, H], h bf16 bits [M, H], fp8 codes [M, H], fp32 scale [M])."""
+    r = _u16(residual_bits)
+    M, H = r.shape
+    br = _u16(branch_bits)
+    w = _u16(weight_bits).reshape(-1)
+    g, ldg = _table(gate_bits)
+    sh, ldsh = _table(shift_bits)
+    sc, ldsc = _table(scale_bits)
+    idx = np.ascontiguousarray(np.asarray(indices).reshape(-1), dtype=np.int64)
+    assert idx.size == M and w.size == H and br.shape == (M, H) and g.shape[1] == sh.shape[1] == sc.shape[1] == H
+    assert M == 0 or (idx.min() >= 0 and idx.max() < min(g.shape[0], sh.shape[0], sc.shape[0]))
+    ro = np.empty((M, H), dtype=np.uint16)
+    h = np.empty((M, H), dtype=np.uint16)
+    q = np.empty((M, H), dtype=np.uint8)
+    s = np.empty((M,), dtype=np.float32)
+    lib().oracle_gate_rms_quant(_p(r), H, _p(g), ldg, _p(br), H, _p(w), _p(sh), ldsh, _p(sc), ldsc, _p(idx), M, H,
+                                float(eps), _p(ro), _p(h), _p(q), _p(s))
+    return ro, h, q, s

@@ -150,3 +150,32 @@ def check_close_swiglu(h: torch.Tensor, acc_exact: np.ndarray, sa, sb, absum: np
     eq = float(np.mean(bits16(h) == h_ref_bits))
     assert eq >= min_equal, eq
     return eq
+
+
+def mod_inputs(M: int, H: int, seed: int, B: int = 6, std_scale: float = 1.0):
+    """Seeded operands of the RMSNorm + AdaLN producers, shaped like the reference's tests/test_fp8_quant_fuse_gpu.py
+    :40-48: rows with log-normal magnitudes, weight ~ 1 + 0.1 N(0, 1), shift / scale / gate as chunk views of one
+    [B, 6H] modulation table (row stride 6H), indices in [0, B).  CPU tensors: x, weight, shift, scale, gate, idx."""
+    g = torch.Generator().manual_seed(seed)
+    mag = torch.exp(torch.randn(M, 1, generator=g) * 1.5)
+    x = (torch.randn(M, H, generator=g) * mag).to(torch.bfloat16)
+    weight = (1.0 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    ada = (torch.randn(B, 6 * H, generator=g) * std_scale).to(torch.bfloat16)
+    shift, scale, gate = ada[:, :H], ada[:, H:2 * H], ada[:, 2 * H:3 * H]
+    idx = torch.randint(0, B, (M,), generator=g)
+    return x, weight, shift, scale, gate, idx
+
+
+def standin_rms(x, weight, shift, scale, idx, eps):
+    """The stock rms_norm_indexed_scale_shift as the reference's CPU stand-in evaluates it (torch CPU ops,
+    tests/fake_h3_consumers.py:77-84): bf16 [M, H]."""
+    xf = x.float()
+    var = (xf * xf).sum(dim=1, keepdim=True) / x.shape[1]
+    n = xf * torch.rsqrt(var + eps) * weight.float()
+    return (n * (1.0 + scale.index_select(0, idx).float()) + shift.index_select(0, idx).float()).to(torch.bfloat16)
+
+
+def standin_gate_rms(residual, gate, branch, weight, shift, scale, idx, eps):
+    """The stock indexed_gate_rms_norm_scale_shift as the CPU stand-in evaluates it (fake_h3_consumers.py:66-74)."""
+    upd = (residual.float() + gate.index_select(0, idx).float() * branch.float()).to(torch.bfloat16)
+    return upd, standin_rms(upd, weight, shift, scale, idx, eps)

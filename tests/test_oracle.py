@@ -296,3 +296,158 @@ def test_dequant_matmul_k_ascending_fp32():
         ref = (ref + (a[:, k:k + 1] * w[None, :, k]).astype(np.float32)).astype(np.float32)
     assert np.array_equal(O.dequant_matmul(ac, wc), ref)
 
+
+
+# ---- the producers with the quant fused in (RMSNorm + AdaLN modulation -> per-token quant) ---------------------------
+
+from _util import bits16, mod_inputs, standin_gate_rms, standin_rms  # noqa: E402
+
+BF16 = torch.bfloat16
+
+
+def _bf(vals):
+    return bits16(torch.as_tensor(vals, dtype=torch.float32).to(BF16))
+
+
+def test_row_sumsq_is_the_exact_sum():
+    """Rows whose squares span few binades: the fp64 sum is exact in any order, so the oracle's total equals math.fsum
+    of the exact squares; rows whose squares span ~50 binades: the fp64 sum rounds, its fp32 rounding is still the
+    correctly rounded sum."""
+    import math
+    rng = np.random.default_rng(3)
+    for H in (8, 64, 520, 5376, 8192):
+        for spread in (1.0, 4.0):
+            x = (rng.standard_normal(H) * np.exp(rng.standard_normal(H) * spread)).astype(np.float32)
+            xb = O.bf16_rne(x)
+            xf = O.bf16_to_f32(xb).astype(np.float64)
+            exact = math.fsum(v * v for v in xf)
+            s = O.row_sumsq(xb)
+            if spread == 1.0:
+                assert s == exact
+            assert np.float32(s) == np.float32(exact)
+
+
+def test_rms_constant_rows_closed_form():
+    """x_k = c, weight 1, shift 0, scale 0, eps 0: var = c^2, r = 1 / |c|, h = sign(c) exactly (c * fl(1/|c|) rounds
+    to +-1 in bf16 for every bf16 c); weight 2 doubles it.  A wrong divisor (H), a dropped rsqrt or a swapped operand
+    gives another value."""
+    for H in (8, 64, 1000, 5376):
+        cs = np.array([1.0, -1.0, 2.0 ** -60, 3.0, -7.5, 1e10, 0.3, -1e-20], np.float32)
+        x = np.repeat(_bf(cs)[:, None], H, axis=1)
+        M = x.shape[0]
+        zeros = np.zeros((1, H), np.uint16)
+        for w, want in ((1.0, 1.0), (2.0, 2.0)):
+            h, q, s = O.rms_quant(x, _bf(np.full(H, w)), zeros, zeros, np.zeros(M, np.int64), 0.0)
+            ref = _bf(np.sign(cs)[:, None] * want * np.ones((1, H)))
+            assert np.array_equal(h, ref), (H, w)
+
+
+def test_rms_zero_rows_give_shift():
+    """x = 0: var = 0, r = 1/sqrt(eps), every product is +-0, so h = bf16(+-0 + shift) = shift for nonzero shift."""
+    H = 256
+    x = np.zeros((3, H), np.uint16)
+    rng = np.random.default_rng(4)
+    sh = _bf(rng.standard_normal((2, H)) + 0.01)
+    sc = _bf(rng.standard_normal((2, H)))
+    h, q, s = O.rms_quant(x, _bf(np.ones(H)), sh, sc, np.array([1, 0, 1]), 1e-6)
+    assert np.array_equal(h, sh[[1, 0, 1]])
+
+
+def test_rms_power_of_two_scale_invariance():
+    """eps = 0: scaling a row by 2^k scales var by 4^k, sqrt by 2^k and r by 2^-k exactly, so h, q and the scale do
+    not change."""
+    x, w, sh, sc, _, idx = mod_inputs(16, 1024, seed=5)
+    base = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), 0.0)
+    for k in (-20, -3, 5, 30):
+        xs = (x.float() * 2.0 ** k).to(BF16)
+        out = O.rms_quant(bits16(xs), bits16(w), bits16(sh), bits16(sc), idx.numpy(), 0.0)
+        for a, b in zip(base, out):
+            assert np.array_equal(a, b), k
+
+
+def test_rms_modulation_order_known_answer():
+    """A row that normalises to exactly 3 (constant 4.0, weight 3, eps 0): h = bf16(3 * (1 + scale) + shift) with each
+    fp32 operation rounded -- numpy's fp32 arithmetic; swapping shift and scale changes it."""
+    H = 512
+    rng = np.random.default_rng(6)
+    sh = _bf(rng.standard_normal((1, H)) * 3)
+    sc = _bf(rng.standard_normal((1, H)) * 3)
+    x = np.repeat(_bf([4.0])[:, None], H, axis=1)
+    h, _, _ = O.rms_quant(x, _bf(np.full(H, 3.0)), sh, sc, np.zeros(1, np.int64), 0.0)
+    g = np.float32(1.0) + O.bf16_to_f32(sc[0]).astype(np.float32)
+    o = np.float32(3.0) * g + O.bf16_to_f32(sh[0]).astype(np.float32)
+    assert np.array_equal(h[0], O.bf16_rne(o.astype(np.float32)))
+    swapped = np.float32(3.0) * (np.float32(1.0) + O.bf16_to_f32(sh[0])) + O.bf16_to_f32(sc[0])
+    assert not np.array_equal(h[0], O.bf16_rne(swapped.astype(np.float32)))
+
+
+def test_rms_index_mapping():
+    """Row m uses table row indices[m]: each row equals the same computation with that table row alone at index 0."""
+    x, w, sh, sc, _, idx = mod_inputs(12, 256, seed=7, B=5)
+    h, q, s = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), 1e-6)
+    for m in range(12):
+        i = int(idx[m])
+        h1, q1, s1 = O.rms_quant(bits16(x[m:m + 1]), bits16(w), bits16(sh[i:i + 1]), bits16(sc[i:i + 1]),
+                                 np.zeros(1, np.int64), 1e-6)
+        assert np.array_equal(h[m], h1[0]) and np.array_equal(q[m], q1[0]) and s[m] == s1[0]
+
+
+def _check_against_standin(x, h, h_ref, w, sc, idx, eps):
+    """Rows whose fp32 sum of squares is the same in both: bit-identical modulated rows (every other operation is the
+    same fp32 arithmetic).  Rows where torch's fp32 sum differs from the correctly rounded one: r moves by a few fp32
+    ulps, so each element within one bf16 ulp plus 2^-20 of |n * (1 + scale)|."""
+    xf = x.float()
+    torch_ss = (xf * xf).sum(dim=1).numpy()
+    ours = np.array([np.float32(O.row_sumsq(r)) for r in bits16(x)])
+    same = torch_ss.view(np.uint32) == ours.view(np.uint32)
+    assert same.mean() > 0.5
+    assert np.array_equal(h[same], bits16(h_ref)[same])
+    if (~same).any():
+        var = (xf * xf).sum(dim=1, keepdim=True) / x.shape[1]
+        big = (xf * torch.rsqrt(var + eps) * w.float() * (1.0 + sc.index_select(0, idx).float())).abs().numpy()
+        a, b = O.bf16_to_f32(h).astype(np.float64), O.bf16_to_f32(bits16(h_ref)).astype(np.float64)
+        tol = np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + big * 2.0 ** -20
+        assert (np.abs(a - b) <= tol)[~same].all()
+
+
+@pytest.mark.parametrize("H", [1024, 5376])
+def test_rms_matches_the_torch_standin(H):
+    """torch's CPU evaluation of the stock producer (tests/fake_h3_consumers.py:77-84); q / scale are quant_rows of h."""
+    x, w, sh, sc, _, idx = mod_inputs(200, H, seed=H)
+    h, q, s = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), 1e-6)
+    _check_against_standin(x, h, standin_rms(x, w, sh, sc, idx, 1e-6), w, sc, idx, 1e-6)
+    q2, s2 = O.quant_rows(h)
+    assert np.array_equal(q, q2) and np.array_equal(s.view(np.uint32), s2.view(np.uint32))
+
+
+def test_gate_rms_residual_and_composition():
+    """residual_out = bf16(residual + gate[i] * branch) equals torch's CPU stand-in bit for bit; h / q / scale equal
+    rms_quant applied to residual_out; the modulated row agrees with the stand-in's as in the plain form."""
+    H = 3072
+    x, w, sh, sc, gt, idx = mod_inputs(150, H, seed=8)
+    br = (torch.randn(150, H, generator=torch.Generator().manual_seed(9)) * 3).to(BF16)
+    ro, h, q, s = O.gate_rms_quant(bits16(x), bits16(gt), bits16(br), bits16(w), bits16(sh), bits16(sc), idx.numpy(),
+                                   1e-6)
+    r_ref, h_ref = standin_gate_rms(x, gt, br, w, sh, sc, idx, 1e-6)
+    assert np.array_equal(ro, bits16(r_ref))
+    h2, q2, s2 = O.rms_quant(ro, bits16(w), bits16(sh), bits16(sc), idx.numpy(), 1e-6)
+    assert np.array_equal(h, h2) and np.array_equal(q, q2) and np.array_equal(s.view(np.uint32), s2.view(np.uint32))
+    _check_against_standin(r_ref, h, h_ref, w, sc, idx, 1e-6)
+
+
+def test_rms_nonfinite_rows():
+    """A NaN in a row makes var NaN: every h of the row is NaN.  An infinity makes var infinite and r = 0: that element
+    is inf * 0 = NaN, the others +-0 + shift = shift.  Both rows get a NaN scale and NaN codes where h is NaN."""
+    x, w, sh, sc, _, idx = mod_inputs(4, 64, seed=10)
+    xb = bits16(x).copy()
+    xb[1, 3] = 0x7FC0
+    xb[2, 5] = 0x7F80
+    h, q, s = O.rms_quant(xb, bits16(w), bits16(sh), bits16(sc), idx.numpy(), 1e-6)
+    nan = (h & 0x7FFF) > 0x7F80
+    assert nan[1].all() and np.isnan(s[1]) and ((q[1] & 0x7F) == 0x7F).all()
+    assert nan[2, 5] and nan[2].sum() == 1 and np.isnan(s[2]) and (q[2, 5] & 0x7F) == 0x7F
+    shift2 = bits16(sh)[int(idx[2])]
+    keep = np.arange(64) != 5
+    nz = (shift2 & 0x7FFF) != 0
+    assert np.array_equal(h[2][keep & nz], shift2[keep & nz])
+    assert np.isfinite(s[[0, 3]]).all()

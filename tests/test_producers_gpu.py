@@ -1,0 +1,144 @@
+"""The per-token quant fused into its producers (RMSNorm + AdaLN modulation; gated residual + RMSNorm + AdaLN
+modulation) against the oracle, bit for bit: fp8 bytes, scale bits, the modulated bf16 row (placeholder mode) and
+residual_out.
+
+Follows the reference's tests/test_fp8_quant_fuse_gpu.py:40-80 (serving-like magnitudes, [B, 6H] modulation tables
+read through chunk views, M = 1 / 200 / 1000 / 4100, both placeholder modes) plus ragged widths, int32 / strided
+indices and directed rows (zero, NaN, inf, subnormal, overflowing squares, an index out of range).
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_quant_equal, bits16, mod_inputs
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+EPS = 1e-6
+
+
+def _nan_aware_equal(out_bits: np.ndarray, ref_bits: np.ndarray, what: str):
+    nan_ref = (ref_bits & 0x7FFF) > 0x7F80
+    assert np.array_equal((out_bits & 0x7FFF) > 0x7F80, nan_ref), f"{what}: NaN positions differ"
+    bad = (out_bits != ref_bits) & ~nan_ref
+    assert not bad.any(), f"{what}: {int(bad.sum())} bf16 values differ, first at {np.argwhere(bad)[:5].tolist()}"
+
+
+def _tables(dev, *views):
+    """The modulation-table views on the device with their row stride kept: the [B, 6H] tensor they slice is moved
+    once and sliced again there (``.to`` of a view would make it contiguous)."""
+    base = views[0]._base
+    assert base is not None and all(v._base is base for v in views)
+    bd = base.to(dev)
+    H = views[0].shape[1]
+    out = []
+    for v in views:
+        off = v.storage_offset() - base.storage_offset()
+        out.append(bd[:, off:off + H])
+        assert out[-1].stride(0) == 6 * H
+    return out
+
+
+def _directed(x: torch.Tensor) -> torch.Tensor:
+    """Rows 0-5 of x replaced by: zeros, a NaN, an inf, subnormals, squares that overflow fp32, one huge outlier."""
+    x = x.clone()
+    M, H = x.shape
+    if M < 6:
+        return x
+    x[0] = 0.0
+    x[1, H // 3] = float("nan")
+    x[2, H - 1] = float("inf")
+    x[3] = torch.full((H,), 1e-39).to(BF16) * torch.sign(x[3].float() + 0.5).to(BF16)
+    x[4, :4] = 2e19
+    x[5, 7] = 3e4
+    return x
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("M,H", [(1, 3072), (200, 5376), (1000, 3072), (4100, 5376), (37, 8192), (300, 1000),
+                                 (77, 520), (9, 8)])
+def test_rms_quant(cuda, M, H, mode):
+    from h3_tp2_amd import ops
+    x, w, sh, sc, _, idx = mod_inputs(M, H, seed=M + H)
+    x = _directed(x)
+    ph = torch.full((M, H), float("nan"), dtype=BF16, device=cuda) if mode else None
+    q, s = ops.rms_quant(x.to(cuda), w.to(cuda), *_tables(cuda, sh, sc), idx.to(cuda), EPS, ph)
+    torch.cuda.synchronize()
+    h_ref, q_ref, s_ref = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
+    assert q.shape == (M, H) and s.shape == (M, 1)
+    assert_quant_equal(q, s, q_ref, s_ref)
+    if mode:
+        _nan_aware_equal(bits16(ph), h_ref, "h")
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("M,H", [(1, 3072), (200, 5376), (1000, 3072), (4100, 5376), (37, 8192), (300, 1000),
+                                 (9, 8)])
+def test_gate_rms_quant(cuda, M, H, mode):
+    from h3_tp2_amd import ops
+    x, w, sh, sc, gt, idx = mod_inputs(M, H, seed=M + H + 1)
+    x = _directed(x)
+    br = (torch.randn(M, H, generator=torch.Generator().manual_seed(M)) * 3).to(BF16)
+    ph = torch.full((M, H), float("nan"), dtype=BF16, device=cuda) if mode else None
+    gd, shd, scd = _tables(cuda, gt, sh, sc)
+    res, q, s = ops.gate_rms_quant(x.to(cuda), gd, br.to(cuda), w.to(cuda), shd, scd, idx.to(cuda), EPS, ph)
+    torch.cuda.synchronize()
+    r_ref, h_ref, q_ref, s_ref = O.gate_rms_quant(bits16(x), bits16(gt), bits16(br), bits16(w), bits16(sh),
+                                                  bits16(sc), idx.numpy(), EPS)
+    _nan_aware_equal(bits16(res), r_ref, "residual_out")
+    assert_quant_equal(q, s, q_ref, s_ref)
+    if mode:
+        _nan_aware_equal(bits16(ph), h_ref, "h")
+
+
+def test_index_forms_and_strided_rows(cuda):
+    """int32 indices, a strided index vector, x rows with a stride past H."""
+    from h3_tp2_amd import ops
+    M, H = 300, 3072
+    x, w, sh, sc, gt, idx = mod_inputs(M, H, seed=11, B=9)
+    xpad = torch.zeros(M, H + 64, dtype=BF16)
+    xpad[:, :H] = x
+    idx2 = torch.stack([idx, torch.zeros_like(idx)], dim=1).reshape(-1)[::2]      # stride 2
+    assert idx2.stride(0) == 2
+    h_ref, q_ref, s_ref = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
+    for ind in (idx.to(torch.int32).to(cuda), idx2.to(cuda)):
+        q, s = ops.rms_quant(xpad.to(cuda)[:, :H], w.to(cuda), *_tables(cuda, sh, sc), ind, EPS)
+        torch.cuda.synchronize()
+        assert_quant_equal(q, s, q_ref, s_ref)
+
+
+def test_index_out_of_range_poisons_only_its_row(cuda):
+    """An index past the tables is not read through: that row's outputs are NaN, the other rows are unchanged."""
+    from h3_tp2_amd import ops
+    M, H = 16, 1024
+    x, w, sh, sc, gt, idx = mod_inputs(M, H, seed=12, B=4)
+    bad = idx.clone()
+    bad[5] = 4
+    bad[9] = -1
+    br = (torch.randn(M, H, generator=torch.Generator().manual_seed(3))).to(BF16)
+    ph = torch.empty((M, H), dtype=BF16, device=cuda)
+    res, q, s = ops.gate_rms_quant(x.to(cuda), gt.to(cuda), br.to(cuda), w.to(cuda), sh.to(cuda), sc.to(cuda),
+                                   bad.to(cuda), EPS, ph)
+    torch.cuda.synchronize()
+    ok = [m for m in range(M) if m not in (5, 9)]
+    r_ref, h_ref, q_ref, s_ref = O.gate_rms_quant(bits16(x[ok]), bits16(gt), bits16(br[ok]), bits16(w), bits16(sh),
+                                                  bits16(sc), idx[ok].numpy(), EPS)
+    assert np.array_equal(bits16(res)[ok], r_ref) and np.array_equal(bits16(ph)[ok], h_ref)
+    qb, sf = q.view(torch.uint8).cpu(), s.cpu()
+    assert_quant_equal(qb[ok], sf[ok], q_ref, s_ref)
+    for m in (5, 9):
+        assert ((bits16(res)[m] & 0x7FFF) > 0x7F80).all() and ((bits16(ph)[m] & 0x7FFF) > 0x7F80).all()
+        assert torch.isnan(sf[m]).item() and ((qb[m] & 0x7F) == 0x7F).all()
+
+
+def test_argument_errors(cuda):
+    from h3_tp2_amd import _lib, ops
+    x, w, sh, sc, _, idx = mod_inputs(4, 1004, seed=13)                   # H % 8 != 0
+    with pytest.raises(_lib.H3Fp8Error, match="multiple of 8"):
+        ops.rms_quant(x.to(cuda), w.to(cuda), sh.to(cuda), sc.to(cuda), idx.to(cuda), EPS)
+    x, w, sh, sc, _, idx = mod_inputs(4, 64, seed=13)
+    with pytest.raises(ValueError, match="indices"):
+        ops.rms_quant(x.to(cuda), w.to(cuda), sh.to(cuda), sc.to(cuda), idx.float().to(cuda), EPS)
+    q, s = ops.rms_quant(x[:0].to(cuda), w.to(cuda), sh.to(cuda), sc.to(cuda), idx[:0].to(cuda), EPS)
+    assert q.shape == (0, 64) and s.shape == (0, 1)
