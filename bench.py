@@ -7,10 +7,10 @@ per token to e4m3fn (kernel 1), then the scaled FP8 GEMM against the per-channel
 with a bf16 output (kernel 2).  A step is one quant + one GEMM over the whole token sequence, inputs resident in HBM;
 ``value`` = 2 M N K / (step time) in TFLOP/s.  ``roofline`` is the GEMM kernel alone against the FP8 dense MFMA peak
 (5.0 PFLOP/s), its average launch time measured with HIP events on the launch stream.  The other measured workloads
-(the single linear, the fused FFN and the 15 s block chain at 1344x768, the grouped launch, and the quant / SwiGLU-tail
-passes against the 8 TB/s HBM peak) are reported under ``workloads``.  ``cpu_baseline`` times the CPU oracle of the
-reference's torch CPU path (per-token quant, fp32 product, scaled epilogue) on a row slice of the headline workload on
-this host's cores, scaled to the full token count.  Synthetic seeded inputs, random-init weights (no checkpoints).
+(the single linear, the fused FFN and the 15 s block chain at 1344x768, the grouped launch, the quant / SwiGLU-tail
+passes and the producers with the quant fused in, against the 8 TB/s HBM peak) are reported under ``workloads``.
+``cpu_baseline`` times the CPU oracle of the reference's torch CPU path (per-token quant, fp32 product, scaled
+epilogue) on a row slice of the headline workload on this host's cores, scaled to the full token count.  Synthetic seeded inputs, random-init weights (no checkpoints).
 """
 from __future__ import annotations
 
@@ -230,6 +230,45 @@ def main() -> None:
         f5 = sum(2.0 * Mg * Ng * Kg for Mg, Kg, Ng, _ in groups)
         out["c5_grouped_one_launch"] = {"ms": round(t, 4), "TFLOP/s": round(f5 / (t * 1e-3) / 1e12, 1)}
         del probs, xs
+
+    if want("producers"):
+        # The quant fused into its producers: norm1 + AdaLN -> QKV input at the 960x576 5 s token count, the gated
+        # residual + norm2 + AdaLN -> fc1 input at the 1344x768 5 s count; H = 3072, a [6, 6H] modulation table.
+        H = K
+        gen = torch.Generator(device=dev).manual_seed(7)
+        res = {}
+        for name, Mp, gate in (("qkv_rms_quant_16740x3072", M, False), ("fc1_gate_rms_quant_31248x3072",
+                                                                         synthetic.CONFIGS["c3_ffn_1344x768_5s"]["M"],
+                                                                         True)):
+            xp = (torch.randn(Mp, H, device=dev, generator=gen)
+                  * torch.exp(torch.randn(Mp, 1, device=dev, generator=gen))).to(torch.bfloat16)
+            wn = (1.0 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16)
+            ada = torch.randn(6, 6 * H, device=dev, generator=gen).to(torch.bfloat16)
+            shp, scp, gtp = ada[:, :H], ada[:, H:2 * H], ada[:, 2 * H:3 * H]
+            idx = torch.randint(0, 6, (Mp,), device=dev, generator=gen)
+            if gate:
+                br = torch.randn(Mp, H, device=dev, generator=gen).to(torch.bfloat16)
+                fused = lambda: ops.gate_rms_quant(xp, gtp, br, wn, shp, scp, idx, 1e-6)  # noqa: E731
+
+                def unfused():
+                    _, hh = ops.indexed_gate_rms_norm_scale_shift(xp, gtp, br, wn, shp, scp, idx, 1e-6)
+                    ops.quant_rows(hh)
+                nbytes = 7.0 * Mp * H + 4.0 * Mp          # residual, branch, residual_out (bf16) + q + scale
+            else:
+                fused = lambda: ops.rms_quant(xp, wn, shp, scp, idx, 1e-6)  # noqa: E731
+
+                def unfused():
+                    ops.quant_rows(ops.rms_norm_indexed_scale_shift(xp, wn, shp, scp, idx, 1e-6))
+                nbytes = 3.0 * Mp * H + 4.0 * Mp          # x (bf16) + q + scale
+            t_f = time_steps(fused, steps, warm) / steps
+            t_u = time_steps(unfused, steps, warm) / steps
+            res[name] = {"ms": round(t_f, 4), "GB/s": round(nbytes / (t_f * 1e-3) / 1e9, 1),
+                         "frac_hbm": round(nbytes / (t_f * 1e-3) / 1e9 / PEAK_GBS, 4),
+                         "unfused_ms": round(t_u, 4), "speedup_vs_unfused": round(t_u / t_f, 3)}
+            del xp, ada, idx
+            if gate:
+                del br
+        out["producers_fused_quant"] = res
 
     # ---- CPU baseline: the oracle of the reference's torch CPU path on a row slice of the headline workload ----
     cpu = None

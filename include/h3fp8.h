@@ -140,6 +140,7 @@ int h3fp8_silu_mul_quant(const void* x, int64_t ldx, int64_t M, int64_t F, void*
  *   var = fp32(sum_k x_k^2) / H; r = 1 / sqrt(var + eps)
  *   h = bf16(((x * r) * weight) * (1 + scale[i]) + shift[i]), every fp32 operation rounded on its own
  *   q [M, H] e4m3fn, qscale [M]: h3fp8_quant_rows of h; with h_out != NULL h is stored there too (bf16 [M, H]).
+ *   q == NULL (h_out given): h only -- the stock producer itself, with the same arithmetic as the fused form.
  * gate / shift / scale are [n_index, H] bf16 tables with row strides ld_gate / ld_shift / ld_scale (the chunk views
  * of an AdaLN modulation tensor); every bf16 row is 16-byte aligned with a stride that is a multiple of 8 elements.
  * The sum of squares is taken in fp64 and rounded once (exact for rows whose squares span < ~40 binades).  An index

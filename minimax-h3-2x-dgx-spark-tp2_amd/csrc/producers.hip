@@ -13,8 +13,11 @@
 //   q, qscale = kernel 1's per-token quant of h (amax, max(amax / 448, 1/(448*512)), clamp, e4m3fn RNE)
 //
 // One 64-lane wave per row, 4 rows per 256-thread workgroup; lane l owns the 16-byte chunks l + 64 j of the row
-// (coalesced 1 KiB per load instruction), the row stays in VGPRs, both reductions are wave shuffles.  HBM-bound:
-// 3H + 4 bytes per row (7H + 4 for the gate form); weight, shift and scale rows are re-read from the caches.
+// (coalesced 1 KiB per load instruction), the row stays in VGPRs, both reductions are wave shuffles.  Every load is a
+// range-checked buffer load (no branches, so all of a row's loads are in flight together): the row's own loads go
+// out first, then the index and, up to 8 chunks per lane, every weight / shift / scale chunk before the reduction.
+// HBM traffic is 3H + 4 bytes per row (7H + 4 for the gate form); the weight and table rows (3 x 2H bytes per row)
+// come from L2.  Staging the tables in LDS per persistent workgroup was measured slower (fewer rows in flight).
 //
 // An index outside [0, n_index) reads table row 0 instead (no access out of bounds) and poisons the row: residual_out
 // and h are NaN, the scale NaN, the codes NaN -- torch's index_select would raise; a kernel cannot.
@@ -53,8 +56,16 @@ struct RmsArgs {
     int64_t ldh;
 };
 
-__device__ __forceinline__ v4u load16(const uint16_t* row, int64_t c) {
-    return *reinterpret_cast<const v4u*>(row + 8 * c);
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+// Range-checked 16-byte chunk c of a row described by `r` (chunks past the row's end read as zero, stores there are
+// dropped): branch-free, so every load of a wave is in flight at once.
+template <int AUX = 0>
+__device__ __forceinline__ v4u ld16(__amdgpu_buffer_rsrc_t r, int c) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)c * 16u, 0, AUX);
+}
+__device__ __forceinline__ void st16(v4u v, __amdgpu_buffer_rsrc_t r, int c) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (uint32_t)c * 16u, 0, 0);
 }
 
 // Wave-wide fp64 sum (xor butterfly; exact for the sums of squares of a bf16 row in all practical cases).
@@ -81,58 +92,82 @@ __device__ __forceinline__ uint32_t quant_pairs(uint32_t p0, uint32_t p1, float 
 }
 
 template <int CPL, bool FINITE>
-__device__ __forceinline__ void store_q(const v4u h[CPL], float inv, uint8_t* qrow, int lane, int64_t nchunk) {
+__device__ __forceinline__ void store_q(const v4u h[CPL], float inv, __amdgpu_buffer_rsrc_t qr, int lane) {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = lane + 64 * j;
-        if (c < nchunk)
-            reinterpret_cast<uint2*>(qrow)[c] = make_uint2(quant_pairs<FINITE>(h[j][0], h[j][1], inv),
-                                                           quant_pairs<FINITE>(h[j][2], h[j][3], inv));
+        const v2u v = {quant_pairs<FINITE>(h[j][0], h[j][1], inv), quant_pairs<FINITE>(h[j][2], h[j][3], inv)};
+        __builtin_amdgcn_raw_buffer_store_b64(v, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
     }
 }
 
-template <bool GATE, bool WRITE_H, int CPL>
-__global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (m >= a.M) return;
-    const int64_t nchunk = a.H >> 3;                   // 16-byte chunks per row
-    int64_t i = a.idx64 ? reinterpret_cast<const int64_t*>(a.indices)[m * a.idx_stride]
-                        : (int64_t)reinterpret_cast<const int32_t*>(a.indices)[m * a.idx_stride];
-    const bool bad = (uint64_t)i >= (uint64_t)a.n_index;
-    i = bad ? 0 : i;
-    const uint32_t poison = bad ? 0x7fc07fc0u : 0u;     // OR-ed into bf16 pairs: NaN if the index is out of range
-    const uint16_t* xr = a.x + m * a.ldx;
+// Where the weight / shift / scale / gate chunks of a row come from: range-checked buffer loads of the table rows
+// (L2-resident after first use).
+struct GlobalTables {
+    __amdgpu_buffer_rsrc_t w, sh, sc, g;
+};
+__device__ __forceinline__ v4u tab16(const GlobalTables& t, int which, int c) {
+    return ld16(which == 0 ? t.w : which == 1 ? t.sh : which == 2 ? t.sc : t.g, c);
+}
+// One row m processed by one wave.  OUT: bit 0 = the e4m3 row and its scale, bit 1 = the bf16 modulated row (h only:
+// the stock producer itself).  EARLY: every table chunk is fetched together with the row (their latency overlaps the
+// row's instead of following the reduction); above 8 chunks per lane the registers do not allow it.
+// `tables(bad)` returns the row's table source and sets `bad` (index out of range); it is called after the row's own
+// loads are issued, so the index load and the table loads that depend on it overlap the row's latency.
+template <bool GATE, int OUT, int CPL, bool EARLY, class MakeTables>
+__device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, int lane, MakeTables tables) {
+    constexpr bool QUANT = (OUT & 1) != 0, WRITE_H = (OUT & 2) != 0;
+    const uint32_t rb = (uint32_t)a.H * 2u;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + m * a.ldx, rb);
     v4u xv[CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int64_t c = lane + 64 * j;
-        xv[j] = (c < nchunk) ? load16(xr, c) : v4u{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < CPL; ++j) xv[j] = ld16<2>(xr, lane + 64 * j);     // streamed once: non-temporal
+    v4u gv[GATE ? CPL : 1], bv[GATE ? CPL : 1];
     if (GATE) {
-        // u = bf16(residual + gate[i] * branch); residual_out = u; the norm below runs on u
-        const uint16_t* gr = a.gate + i * a.ld_gate;
-        const uint16_t* br = a.branch + m * a.ld_branch;
-        uint16_t* ro = a.residual_out + m * a.ld_res;
+        const __amdgpu_buffer_rsrc_t br = make_rsrc(a.branch + m * a.ld_branch, rb);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int64_t c = lane + 64 * j;
-            if (c < nchunk) {
-                const v4u gv = load16(gr, c), bv = load16(br, c);
-                v4u u;
+        for (int j = 0; j < (GATE ? CPL : 1); ++j) bv[j] = ld16<2>(br, lane + 64 * j);
+    }
+    __builtin_amdgcn_sched_barrier(0);                  // the row's loads go out before the index load
+    bool bad;
+    const auto t = tables(bad);
+    const uint32_t poison = bad ? 0x7fc07fc0u : 0u;     // OR-ed into bf16 pairs: NaN if the index is out of range
+    if (GATE) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const float r0 = u2f(xv[j][k] << 16), r1 = u2f(xv[j][k] & 0xffff0000u);
-                    const float p0 = u2f(gv[k] << 16) * u2f(bv[k] << 16);
-                    const float p1 = u2f(gv[k] & 0xffff0000u) * u2f(bv[k] & 0xffff0000u);
-                    u[k] = cvt_bf16x2(r0 + p0, r1 + p1) | poison;
-                }
-                xv[j] = u;
-                *reinterpret_cast<v4u*>(ro + 8 * c) = u;
-            }
+        for (int j = 0; j < (GATE ? CPL : 1); ++j) gv[j] = tab16(t, 3, lane + 64 * j);
+    }
+    constexpr int NE = EARLY ? CPL : 1;
+    v4u wv_e[NE], sh_e[NE], sc_e[NE];
+    if (EARLY) {
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            wv_e[j] = tab16(t, 0, lane + 64 * j);
+            sh_e[j] = tab16(t, 1, lane + 64 * j);
+            sc_e[j] = tab16(t, 2, lane + 64 * j);
         }
     }
-    // sum of squares: each square is exact in fp32, the fp64 sum rounds once to fp32
+    __builtin_amdgcn_sched_barrier(0);                  // keep every load above the reduction
+    const int nchunk = (int)(a.H >> 3);
+    if (GATE) {
+        // u = bf16(residual + gate[i] * branch); residual_out = u; the norm below runs on u.  Chunks past the row are
+        // forced to +0 (their stores are dropped).
+        const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.residual_out + m * a.ld_res, rb);
+#pragma unroll
+        for (int j = 0; j < (GATE ? CPL : 1); ++j) {
+            const bool in = lane + 64 * j < nchunk;
+            v4u u;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float r0 = u2f(xv[j][k] << 16), r1 = u2f(xv[j][k] & 0xffff0000u);
+                const float p0 = u2f(gv[j][k] << 16) * u2f(bv[j][k] << 16);
+                const float p1 = u2f(gv[j][k] & 0xffff0000u) * u2f(bv[j][k] & 0xffff0000u);
+                u[k] = in ? (cvt_bf16x2(r0 + p0, r1 + p1) | poison) : 0u;
+            }
+            xv[j] = u;
+            st16(u, ro, lane + 64 * j);
+        }
+    }
+    // sum of squares: each square is exact in fp32, the fp64 sum rounds once to fp32 (chunks past the row add +0;
+    // a poisoned row's NaN makes the sum NaN)
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
@@ -152,17 +187,14 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     asm volatile("" : "+v"(one));
     const float r = bad ? u2f(0x7fc00000u) : one / d;  // IEEE division (torch's CPU rsqrt: 1 / sqrt)
     // modulation, bf16 rounding, row maximum
-    const uint16_t* shr = a.shift + i * a.ld_shift;
-    const uint16_t* scr = a.scale + i * a.ld_scale;
     v4u h[CPL];
     uint32_t mx = 0;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = lane + 64 * j;
-        const bool in = c < nchunk;
-        const v4u wv = in ? load16(a.weight, c) : v4u{0u, 0u, 0u, 0u};
-        const v4u sh = in ? load16(shr, c) : v4u{0u, 0u, 0u, 0u};
-        const v4u sc = in ? load16(scr, c) : v4u{0u, 0u, 0u, 0u};
+        const bool in = lane + 64 * j < nchunk;
+        const v4u wv = EARLY ? wv_e[EARLY ? j : 0] : tab16(t, 0, lane + 64 * j);
+        const v4u sh = EARLY ? sh_e[EARLY ? j : 0] : tab16(t, 1, lane + 64 * j);
+        const v4u sc = EARLY ? sc_e[EARLY ? j : 0] : tab16(t, 2, lane + 64 * j);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             float o[2];
@@ -176,43 +208,70 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
                 const float g = one + se;
                 o[e] = n * g + be;
             }
-            h[j][k] = in ? cvt_bf16x2(o[0], o[1]) : 0u;   // columns past H: +0, the maximum is unchanged
+            h[j][k] = in ? cvt_bf16x2(o[0], o[1]) : 0u;   // chunks past the row: +0, the maximum is unchanged
             const uint32_t lo = (h[j][k] << 16) & 0x7fff0000u, hi = h[j][k] & 0x7fff0000u;
             mx = mx > lo ? mx : lo;
             mx = mx > hi ? mx : hi;
         }
     }
-    mx = wave_max_u32(mx);
-    const float s = row_scale(u2f(mx));
-    const float inv = inv_scale(s);
-    uint8_t* qrow = a.q + m * a.ldq;
-    if (__builtin_amdgcn_readfirstlane(mx) < 0x7f800000u) store_q<CPL, true>(h, inv, qrow, lane, nchunk);
-    else store_q<CPL, false>(h, inv, qrow, lane, nchunk);
-    if (WRITE_H) {
-        uint16_t* hr = a.h_out + m * a.ldh;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int64_t c = lane + 64 * j;
-            if (c < nchunk) *reinterpret_cast<v4u*>(hr + 8 * c) = h[j];
-        }
+    float s = 0.0f;
+    if (QUANT) {
+        mx = wave_max_u32(mx);
+        s = row_scale(u2f(mx));
+        const float inv = inv_scale(s);
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + m * a.ldq, (uint32_t)a.H);
+        if (__builtin_amdgcn_readfirstlane(mx) < 0x7f800000u) store_q<CPL, true>(h, inv, qr, lane);
+        else store_q<CPL, false>(h, inv, qr, lane);
     }
-    if (lane == 0) a.qscale[m] = s;
+    if (WRITE_H) {
+        const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.h_out + m * a.ldh, rb);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) st16(h[j], hr, lane + 64 * j);
+    }
+    if (QUANT && lane == 0) a.qscale[m] = s;
 }
 
-template <bool GATE, bool WRITE_H>
-int launch_rms(const RmsArgs& a, hipStream_t st) {
-    const int64_t cpl = ((a.H >> 3) + 63) / 64;
-    dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
-#define H3_R(N) hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, WRITE_H, N>), grid, block, 0, st, a)
-    if (cpl <= 2) H3_R(2);
-    else if (cpl <= 4) H3_R(4);
-    else if (cpl <= 6) H3_R(6);
-    else if (cpl <= 8) H3_R(8);
-    else if (cpl <= 12) H3_R(12);
-    else H3_R(16);
-#undef H3_R
+__device__ __forceinline__ int64_t row_index(const RmsArgs& a, int64_t m, bool& bad) {
+    int64_t i = a.idx64 ? reinterpret_cast<const int64_t*>(a.indices)[m * a.idx_stride]
+                        : (int64_t)reinterpret_cast<const int32_t*>(a.indices)[m * a.idx_stride];
+    bad = (uint64_t)i >= (uint64_t)a.n_index;
+    return bad ? 0 : i;
+}
+
+// Tables read from global memory: one wave per row, 4 rows per 256-thread workgroup.
+template <bool GATE, int OUT, int CPL>
+__global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (m >= a.M) return;
+    rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 8)>(a, m, lane, [&](bool& bad) {
+        const int64_t i = row_index(a, m, bad);
+        const uint32_t rb = (uint32_t)a.H * 2u;
+        GlobalTables t;
+        t.w = make_rsrc(a.weight, rb);
+        t.sh = make_rsrc(a.shift + i * a.ld_shift, rb);
+        t.sc = make_rsrc(a.scale + i * a.ld_scale, rb);
+        t.g = make_rsrc(GATE ? a.gate + i * a.ld_gate : a.weight, rb);
+        return t;
+    });
+}
+
+template <bool GATE, int OUT, int CPL>
+int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL>), dim3((unsigned)((a.M + 3) / 4)), dim3(256), 0, st, a);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
+}
+
+template <bool GATE, int OUT>
+int launch_rms(const RmsArgs& a, hipStream_t st) {
+    const int64_t cpl = ((a.H >> 3) + 63) / 64;
+    if (cpl <= 2) return launch_rms_cpl<GATE, OUT, 2>(a, st);
+    if (cpl <= 4) return launch_rms_cpl<GATE, OUT, 4>(a, st);
+    if (cpl <= 6) return launch_rms_cpl<GATE, OUT, 6>(a, st);
+    if (cpl <= 8) return launch_rms_cpl<GATE, OUT, 8>(a, st);
+    if (cpl <= 12) return launch_rms_cpl<GATE, OUT, 12>(a, st);
+    return launch_rms_cpl<GATE, OUT, 16>(a, st);
 }
 
 int check_rows(const void* p, int64_t ld, int64_t H, const char* what, const char* who) {
@@ -236,9 +295,17 @@ int check_rms(const RmsArgs& a, bool gate, const char* who) {
     if (!rc && a.h_out) rc = check_rows(a.h_out, a.ldh, a.H, "h_out", who);
     if (rc) return rc;
     H3_REQUIRE(a.indices && a.idx_stride >= 0 && a.n_index > 0, "%s: bad indices or empty tables", who);
-    H3_REQUIRE(a.q && a.qscale && a.ldq >= a.H && a.ldq % 8 == 0 && ((uintptr_t)a.q & 7) == 0,
-               "%s: q must be 8-byte aligned with a row stride >= H and a multiple of 8", who);
+    H3_REQUIRE(a.q || a.h_out, "%s: neither q nor h_out given", who);
+    if (a.q)
+        H3_REQUIRE(a.qscale && a.ldq >= a.H && a.ldq % 8 == 0 && ((uintptr_t)a.q & 7) == 0,
+                   "%s: q must be 8-byte aligned with a row stride >= H and a multiple of 8, with a scale vector", who);
     return H3FP8_OK;
+}
+
+template <bool GATE>
+int launch_rms_out(const RmsArgs& a, hipStream_t st) {
+    if (!a.q) return launch_rms<GATE, 2>(a, st);
+    return a.h_out ? launch_rms<GATE, 3>(a, st) : launch_rms<GATE, 1>(a, st);
 }
 
 }  // namespace
@@ -262,7 +329,7 @@ int h3fp8_rms_quant(const void* x, int64_t ldx, const void* weight, const void* 
     int rc = check_rms(a, false, "h3fp8_rms_quant");
     if (rc || M == 0 || H == 0) return rc;
     hipStream_t st = (hipStream_t)stream;
-    return h_out ? launch_rms<false, true>(a, st) : launch_rms<false, false>(a, st);
+    return launch_rms_out<false>(a, st);
 }
 
 int h3fp8_gate_rms_quant(const void* residual, int64_t ldr, const void* gate, int64_t ld_gate, const void* branch,
@@ -286,7 +353,7 @@ int h3fp8_gate_rms_quant(const void* residual, int64_t ldr, const void* gate, in
     int rc = check_rms(a, true, "h3fp8_gate_rms_quant");
     if (rc || M == 0 || H == 0) return rc;
     hipStream_t st = (hipStream_t)stream;
-    return h_out ? launch_rms<true, true>(a, st) : launch_rms<true, false>(a, st);
+    return launch_rms_out<true>(a, st);
 }
 
 }  // extern "C"

@@ -267,6 +267,37 @@ def rms_quant(x: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor, scale:
     return q, s
 
 
+def rms_norm_indexed_scale_shift(x: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                                 indices: torch.Tensor, eps: float) -> torch.Tensor:
+    """The producer alone (bf16 h [M, H], no quant), with the fused form's arithmetic: the drop-in for the stock
+    ``rms_norm_indexed_scale_shift`` (tests/fake_h3_consumers.py:77-84 states its formula)."""
+    M, H, n_index, ib = _producer_args(x, weight, (shift, scale), indices, ("shift", "scale"))
+    h = torch.empty((M, H), device=x.device, dtype=torch.bfloat16)
+    _lib.call("h3fp8_rms_quant", x.data_ptr(), _rows(x, "x"), weight.data_ptr(), shift.data_ptr(),
+              _rows(shift, "shift"), scale.data_ptr(), _rows(scale, "scale"), n_index, indices.data_ptr(),
+              indices.stride(0), ib, M, H, float(eps), None, 0, None, h.data_ptr(), H, _stream(x))
+    return h
+
+
+def indexed_gate_rms_norm_scale_shift(residual: torch.Tensor, gate: torch.Tensor, branch: torch.Tensor,
+                                      weight: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                                      indices: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """The gated producer alone: (residual_out bf16 [M, H], h bf16 [M, H]) with the fused form's arithmetic
+    (tests/fake_h3_consumers.py:66-74 states its formula)."""
+    M, H, n_index, ib = _producer_args(residual, weight, (gate, shift, scale), indices, ("gate", "shift", "scale"))
+    if branch.shape != residual.shape or branch.dtype != torch.bfloat16:
+        raise ValueError("branch must be bfloat16 with the residual's shape")
+    _need_cuda(branch)
+    res = torch.empty((M, H), device=residual.device, dtype=torch.bfloat16)
+    h = torch.empty((M, H), device=residual.device, dtype=torch.bfloat16)
+    _lib.call("h3fp8_gate_rms_quant", residual.data_ptr(), _rows(residual, "residual"), gate.data_ptr(),
+              _rows(gate, "gate"), branch.data_ptr(), _rows(branch, "branch"), weight.data_ptr(), shift.data_ptr(),
+              _rows(shift, "shift"), scale.data_ptr(), _rows(scale, "scale"), n_index, indices.data_ptr(),
+              indices.stride(0), ib, M, H, float(eps), res.data_ptr(), H, None, 0, None, h.data_ptr(), H,
+              _stream(residual))
+    return res, h
+
+
 def gate_rms_quant(residual: torch.Tensor, gate: torch.Tensor, branch: torch.Tensor, weight: torch.Tensor,
                    shift: torch.Tensor, scale: torch.Tensor, indices: torch.Tensor, eps: float,
                    ph: torch.Tensor | None = None):

@@ -142,3 +142,59 @@ def test_argument_errors(cuda):
         ops.rms_quant(x.to(cuda), w.to(cuda), sh.to(cuda), sc.to(cuda), idx.float().to(cuda), EPS)
     q, s = ops.rms_quant(x[:0].to(cuda), w.to(cuda), sh.to(cuda), sc.to(cuda), idx[:0].to(cuda), EPS)
     assert q.shape == (0, 64) and s.shape == (0, 1)
+
+
+def test_block_sites_end_to_end(cuda, monkeypatch):
+    """The qkv and fc1 sites wired on a stand-in DiT block, on the GPU, with own_producers (the stock producers are
+    the kernels' h-only form, so the fused form passes its self-check) and kernel 1 as the layers' quant: the QKV and
+    fc1 layers receive the oracle's fp8 rows and scales, the block returns the oracle's residual_out."""
+    import threading
+
+    from _fake_dit import FakeQuantFP8, make_tr
+    from _util import standin_gate_rms, standin_rms
+    from h3_tp2_amd import fp8_quant_fuse as fq, ops
+
+    st = dict(fq._state)
+    st["checked"], st["disabled"] = {}, set()
+    monkeypatch.setattr(fq, "_state", st)
+    monkeypatch.setattr(fq, "_stats", dict.fromkeys(fq._stats, 0))
+    monkeypatch.setattr(fq, "_tls", threading.local())
+    monkeypatch.setattr(FakeQuantFP8, "forward", FakeQuantFP8.forward)
+    monkeypatch.setattr(FakeQuantFP8, "impl", staticmethod(ops.quant_rows))
+    tr = make_tr(standin_rms, standin_gate_rms)
+    assert fq.install(("qkv", "fc1"), kernel1=False, tr=tr, quant_cls=FakeQuantFP8, lora_types=(),
+                      own_producers=True) == ["qkv", "fc1"]
+    M, H = 1000, 3072
+    x, w, sh, sc, gt, idx = mod_inputs(M, H, seed=21)
+    br = (torch.randn(M, H, generator=torch.Generator().manual_seed(22)) * 3).to(BF16)
+    w2 = (w.float() * 0.75).to(BF16)
+    gd, shd, scd = _tables(cuda, gt, sh, sc)
+    blk = tr.MiniMaxH3DiTBlock(H, w.to(cuda), w2.to(cuda))
+    res = blk(x.to(cuda), br.to(cuda), shd, scd, gd, idx.to(cuda))
+    torch.cuda.synchronize()
+    s = fq.stats()
+    assert (s["fused_qkv"], s["fused_fc1"], s["consumed"], s["materialize"], s["selfcheck_fail"]) == (1, 1, 2, 0, 0)
+    _, q_ref, s_ref = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
+    assert_quant_equal(*blk.attn.qkv_proj.seen[0], q_ref, s_ref)
+    r_ref, _, q2_ref, s2_ref = O.gate_rms_quant(bits16(x), bits16(gt), bits16(br), bits16(w2), bits16(sh),
+                                                bits16(sc), idx.numpy(), EPS)
+    assert_quant_equal(*blk.mlp.fc1.seen[0], q2_ref, s2_ref)
+    assert np.array_equal(bits16(res), r_ref)
+
+
+def test_h_only_form_matches_the_fused_rows(cuda):
+    """The producers without the quant (the own-producer form) give the fused form's bf16 rows bit for bit."""
+    from h3_tp2_amd import ops
+    M, H = 777, 5376
+    x, w, sh, sc, gt, idx = mod_inputs(M, H, seed=23)
+    br = (torch.randn(M, H, generator=torch.Generator().manual_seed(24))).to(BF16)
+    shd, scd, gd = _tables(cuda, sh, sc, gt)
+    h = ops.rms_norm_indexed_scale_shift(x.to(cuda), w.to(cuda), shd, scd, idx.to(cuda), EPS)
+    res, h2 = ops.indexed_gate_rms_norm_scale_shift(x.to(cuda), gd, br.to(cuda), w.to(cuda), shd, scd, idx.to(cuda),
+                                                    EPS)
+    torch.cuda.synchronize()
+    h_ref, _, _ = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
+    r_ref, h2_ref, _, _ = O.gate_rms_quant(bits16(x), bits16(gt), bits16(br), bits16(w), bits16(sh), bits16(sc),
+                                           idx.numpy(), EPS)
+    assert np.array_equal(bits16(h), h_ref)
+    assert np.array_equal(bits16(res), r_ref) and np.array_equal(bits16(h2), h2_ref)
