@@ -7,6 +7,8 @@
 // Design (HBM-bound: 2 bytes read + 1 byte written per element, plus 4 bytes of scale per row):
 //   * one 64-lane wavefront per row; a lane owns CPL chunks of 8 bf16 (16-byte loads), chunk c = lane + 64 j, so every
 //     load instruction of the wave reads 1 KiB of the row contiguously; the row stays in VGPRs (read from HBM once);
+//   * range-checked buffer loads and stores (a per-row descriptor): no branch around the row's tail, so all of a
+//     row's loads are in flight together (guarded global loads made the compiler wait after every second load);
 //   * the row maximum is an integer max over |x| bit patterns (for non-negative floats the integer order is the float
 //     order and every NaN pattern is above +inf, so the max propagates NaN exactly like the reference's), reduced
 //     across the wave with xor-shuffles -- no LDS, no barrier;
@@ -18,6 +20,8 @@
 namespace {
 
 using namespace h3;
+
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 // |x| bit patterns of the 8 bf16 values in a 16-byte chunk, max-reduced to one 16-bit pattern.
 __device__ __forceinline__ uint32_t chunk_absmax(uint4 v) {
@@ -61,15 +65,15 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restr
                                                          float* __restrict__ scale,
                                                          const float* __restrict__ row_amax) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= M) return;
-    const int64_t nchunk = K >> 3;
-    const v4u* xr = reinterpret_cast<const v4u*>(x + row * ldx);
+    // Range-checked buffer accesses: chunks past the row read as zero (|0| does not raise the maximum) and their
+    // stores are dropped, with no branch -- every load of the row is in flight at once.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + row * ldx, (uint32_t)K * 2u);
     uint4 v[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        int64_t c = lane + 64 * j;
-        v4u t = (c < nchunk) ? __builtin_nontemporal_load(xr + c) : v4u{0u, 0u, 0u, 0u};
+        const v4u t = __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)(lane + 64 * j) * 16u, 0, 2);   // nt
         v[j] = make_uint4(t.x, t.y, t.z, t.w);
     }
     float amax;
@@ -87,18 +91,18 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restr
     }
     const float s = row_scale(amax);
     const float inv = inv_scale(s);
-    uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + row * ldq, (uint32_t)K);
     if (__builtin_amdgcn_readfirstlane(f2u(amax) & 0x7fffffffu) < 0x7f800000u) {   // wave-uniform: finite maximum
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            int64_t c = lane + 64 * j;
-            if (c < nchunk) qr[c] = chunk_quant<true>(v[j], inv);
+            const uint2 o = chunk_quant<true>(v[j], inv);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            int64_t c = lane + 64 * j;
-            if (c < nchunk) qr[c] = chunk_quant<false>(v[j], inv);
+            const uint2 o = chunk_quant<false>(v[j], inv);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
         }
     }
     if (lane == 0) scale[row] = s;
