@@ -157,6 +157,43 @@ int h3fp8_gate_rms_quant(const void* residual, int64_t ldr, const void* gate, in
                          float* qscale, void* h_out, int64_t ldh, void* stream);
 
 /*
+ * The consumers of a two-pass GEMM's fp32 product `acc` [M, N] (row stride ld_acc), with the scale pass fused in:
+ * each reads branch[m, n] = bf16(sa[m] * (sb[n] * acc[m, n])) (bias: bf16(fma(sa[m], sb[n] * acc[m, n], bias[n])))
+ * where the stock path would read the scale pass's bf16 output.  sa [M] and sb [N] fp32 contiguous, bias bf16 [N] or
+ * NULL; product rows 16-byte aligned (8-byte for the qk form).
+ *   h3fp8_scale_gate_rms_quant  the out projection's consumer: h3fp8_gate_rms_quant with that branch (q may be NULL:
+ *                               residual_out + h only, the stock consumer's outputs; with q the fc1 input's quant as
+ *                               well).  Replaces fp8_consumers.gate_rms_fused / _scale_indexed_gate_rms_norm_scale_
+ *                               shift_kernel (h3_tp2/fp8_consumers.py:464-485, :242-293).
+ *   h3fp8_scale_indexed_gate    the fc2 projection's consumer indexed_gate: out = bf16(x + gate[i] * branch), rows of
+ *                               H (H % 8 == 0, H <= 8192).  Replaces gate_fused / _scale_indexed_gate_kernel
+ *                               (h3_tp2/fp8_consumers.py:488-504, :204-240).
+ *   h3fp8_scale_qk_norm_rope    the qkv projection's consumer for q and k: per token and head (128 dims, q heads
+ *                               then k heads in the product's columns), n = bf16((x * r) * w) with
+ *                               r = 1 / sqrt(fp32(sum x^2) / 128 + eps), then the half-split rotation of the first 96
+ *                               dims by rope[t] (cos | sin, [T, 96] fp32 if rope_f32 else bf16):
+ *                               out_d = bf16(n_d cos - n_(d+48) sin) (d < 48), bf16(n_d cos + n_(d-48) sin) (d < 96),
+ *                               n_d (d >= 96).  out_q [T, Hq, 128] / out_k [T, Hk, 128] with token / head strides.
+ *                               The v columns take h3fp8_scale_bias_cast.  Replaces qk_norm_rope_fused /
+ *                               _scale_rms_norm_rope_kernel (h3_tp2/fp8_consumers.py:424-461, :131-193).
+ * Sums of squares as in the producers (fp32 squares, fp64 sum, one rounding).
+ */
+int h3fp8_scale_gate_rms_quant(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                               const void* residual, int64_t ldr, const void* gate, int64_t ld_gate,
+                               const void* weight, const void* shift, int64_t ld_shift, const void* scale,
+                               int64_t ld_scale, int64_t n_index, const void* indices, int64_t idx_stride,
+                               int idx_bytes, int64_t M, int64_t H, float eps, void* residual_out, int64_t ld_res,
+                               void* q, int64_t ldq, float* qscale, void* h_out, int64_t ldh, void* stream);
+int h3fp8_scale_indexed_gate(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                             const void* x, int64_t ldx, const void* gate, int64_t ld_gate, int64_t n_index,
+                             const void* indices, int64_t idx_stride, int idx_bytes, int64_t M, int64_t H, void* out,
+                             int64_t ldo, void* stream);
+int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                             int64_t T, int Hq, int Hk, const void* q_weight, const void* k_weight, const void* rope,
+                             int64_t ld_rope, int rope_f32, float eps, void* out_q, int64_t ldq_t, int64_t ldq_h,
+                             void* out_k, int64_t ldk_t, int64_t ldk_h, void* stream);
+
+/*
  * The two-pass scale pass: y = round(sa[m] * (sb[n] * x32[m, n])) (bias: one fma), bf16 or fp16.
  * Replaces fp8_gemm._scale_bias_cast / _launch (h3_tp2/fp8_gemm.py:37-54, :167-171) and the consumers' stash
  * materialisation (h3_tp2/fp8_consumers.py:373-380).

@@ -54,6 +54,13 @@ struct RmsArgs {
     float* qscale;              // fp32 [M]
     uint16_t* h_out;            // optional bf16 [M, H]: the modulated row (the stock producer's output)
     int64_t ldh;
+    // the consumer forms: the branch (gate form's third operand) is the scaled-GEMM epilogue of an fp32 product,
+    // branch = bf16(sa[m] * (sb[n] * acc[m, n])) or bf16(fma(sa[m], sb[n] * acc[m, n], bias[n]))
+    const float* acc;           // fp32 [M, H]
+    int64_t ld_acc;
+    const float* sa;            // fp32 [M], contiguous
+    const float* sb;            // fp32 [H], contiguous
+    const uint16_t* bias;       // bf16 [H] or null
 };
 
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
@@ -113,7 +120,11 @@ __device__ __forceinline__ v4u tab16(const GlobalTables& t, int which, int c) {
 // row's instead of following the reduction); above 8 chunks per lane the registers do not allow it.
 // `tables(bad)` returns the row's table source and sets `bad` (index out of range); it is called after the row's own
 // loads are issued, so the index load and the table loads that depend on it overlap the row's latency.
-template <bool GATE, int OUT, int CPL, bool EARLY, class MakeTables>
+//
+// B32 (gate form only): the branch is the scaled-GEMM epilogue of the fp32 product `acc` (the consumer of the out /
+// fc2 projection reading the accumulator instead of a bf16 output).  NORM = false stops after residual_out: that is
+// the fc2 site's indexed_gate, out = bf16(x + gate[i] * branch).
+template <bool GATE, int OUT, int CPL, bool EARLY, bool B32, bool NORM, class MakeTables>
 __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, int lane, MakeTables tables) {
     constexpr bool QUANT = (OUT & 1) != 0, WRITE_H = (OUT & 2) != 0;
     const uint32_t rb = (uint32_t)a.H * 2u;
@@ -122,10 +133,26 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
 #pragma unroll
     for (int j = 0; j < CPL; ++j) xv[j] = ld16<2>(xr, lane + 64 * j);     // streamed once: non-temporal
     v4u gv[GATE ? CPL : 1], bv[GATE ? CPL : 1];
-    if (GATE) {
+    constexpr int NB = B32 ? CPL : 1;
+    v4u a_lo[NB], a_hi[NB], s_lo[NB], s_hi[NB], b_e[NB];
+    if (GATE && !B32) {
         const __amdgpu_buffer_rsrc_t br = make_rsrc(a.branch + m * a.ld_branch, rb);
 #pragma unroll
         for (int j = 0; j < (GATE ? CPL : 1); ++j) bv[j] = ld16<2>(br, lane + 64 * j);
+    }
+    if (GATE && B32) {
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.acc + m * a.ld_acc, 2u * rb);
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sb, 2u * rb);
+        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(a.bias ? a.bias : a.weight, a.bias ? rb : 0u);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t c = (uint32_t)(lane + 64 * j);
+            a_lo[j] = __builtin_amdgcn_raw_buffer_load_b128(ar, c * 32u, 0, 2);
+            a_hi[j] = __builtin_amdgcn_raw_buffer_load_b128(ar, c * 32u + 16u, 0, 2);
+            s_lo[j] = __builtin_amdgcn_raw_buffer_load_b128(sr, c * 32u, 0, 0);
+            s_hi[j] = __builtin_amdgcn_raw_buffer_load_b128(sr, c * 32u + 16u, 0, 0);
+            b_e[j] = __builtin_amdgcn_raw_buffer_load_b128(bsr, c * 16u, 0, 0);   // zeros without a bias
+        }
     }
     __builtin_amdgcn_sched_barrier(0);                  // the row's loads go out before the index load
     bool bad;
@@ -147,6 +174,26 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
     }
     __builtin_amdgcn_sched_barrier(0);                  // keep every load above the reduction
     const int nchunk = (int)(a.H >> 3);
+    if (GATE && B32) {
+        // branch = bf16(epilogue(acc)): t = sb * acc, then sa * t or fma(sa, t, bias), one rounding (the scale pass)
+        const float sam = a.sa[m];
+        const bool hb = a.bias != nullptr;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            float y[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float acc = u2f(e < 4 ? a_lo[j][e] : a_hi[j][e - 4]);
+                const float sbn = u2f(e < 4 ? s_lo[j][e] : s_hi[j][e - 4]);
+                const uint32_t bw = b_e[j][e >> 1];
+                const float b = u2f((e & 1) ? (bw & 0xffff0000u) : (bw << 16));
+                const float t = sbn * acc;
+                y[e] = hb ? __builtin_fmaf(sam, t, b) : sam * t;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) bv[j][k] = cvt_bf16x2(y[2 * k], y[2 * k + 1]);
+        }
+    }
     if (GATE) {
         // u = bf16(residual + gate[i] * branch); residual_out = u; the norm below runs on u.  Chunks past the row are
         // forced to +0 (their stores are dropped).
@@ -166,6 +213,7 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
             st16(u, ro, lane + 64 * j);
         }
     }
+    if (!NORM) return;
     // sum of squares: each square is exact in fp32, the fp64 sum rounds once to fp32 (chunks past the row add +0;
     // a poisoned row's NaN makes the sum NaN)
     double ss = 0.0;
@@ -239,12 +287,12 @@ __device__ __forceinline__ int64_t row_index(const RmsArgs& a, int64_t m, bool& 
 }
 
 // Tables read from global memory: one wave per row, 4 rows per 256-thread workgroup.
-template <bool GATE, int OUT, int CPL>
+template <bool GATE, int OUT, int CPL, bool B32 = false, bool NORM = true>
 __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     const int lane = threadIdx.x & 63;
     const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (m >= a.M) return;
-    rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 8)>(a, m, lane, [&](bool& bad) {
+    rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 8 && !B32), B32, NORM>(a, m, lane, [&](bool& bad) {
         const int64_t i = row_index(a, m, bad);
         const uint32_t rb = (uint32_t)a.H * 2u;
         GlobalTables t;
@@ -256,22 +304,23 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     });
 }
 
-template <bool GATE, int OUT, int CPL>
+template <bool GATE, int OUT, int CPL, bool B32, bool NORM>
 int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL>), dim3((unsigned)((a.M + 3) / 4)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, NORM>), dim3((unsigned)((a.M + 3) / 4)), dim3(256), 0,
+                       st, a);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
 
-template <bool GATE, int OUT>
+template <bool GATE, int OUT, bool B32 = false, bool NORM = true>
 int launch_rms(const RmsArgs& a, hipStream_t st) {
     const int64_t cpl = ((a.H >> 3) + 63) / 64;
-    if (cpl <= 2) return launch_rms_cpl<GATE, OUT, 2>(a, st);
-    if (cpl <= 4) return launch_rms_cpl<GATE, OUT, 4>(a, st);
-    if (cpl <= 6) return launch_rms_cpl<GATE, OUT, 6>(a, st);
-    if (cpl <= 8) return launch_rms_cpl<GATE, OUT, 8>(a, st);
-    if (cpl <= 12) return launch_rms_cpl<GATE, OUT, 12>(a, st);
-    return launch_rms_cpl<GATE, OUT, 16>(a, st);
+    if (cpl <= 2) return launch_rms_cpl<GATE, OUT, 2, B32, NORM>(a, st);
+    if (cpl <= 4) return launch_rms_cpl<GATE, OUT, 4, B32, NORM>(a, st);
+    if (cpl <= 6) return launch_rms_cpl<GATE, OUT, 6, B32, NORM>(a, st);
+    if (cpl <= 8) return launch_rms_cpl<GATE, OUT, 8, B32, NORM>(a, st);
+    if (cpl <= 12) return launch_rms_cpl<GATE, OUT, 12, B32, NORM>(a, st);
+    return launch_rms_cpl<GATE, OUT, 16, B32, NORM>(a, st);
 }
 
 int check_rows(const void* p, int64_t ld, int64_t H, const char* what, const char* who) {
@@ -281,20 +330,29 @@ int check_rows(const void* p, int64_t ld, int64_t H, const char* what, const cha
     return H3FP8_OK;
 }
 
-int check_rms(const RmsArgs& a, bool gate, const char* who) {
+// gate: the gated forms; b32: the branch is an fp32 product; norm: the RMSNorm + modulation (+ quant) follows.
+int check_rms(const RmsArgs& a, bool gate, bool b32, bool norm, const char* who) {
     H3_REQUIRE(a.M >= 0 && a.H >= 0, "%s: negative size", who);
     H3_REQUIRE(a.H % 8 == 0 && a.H <= 8192, "%s: H=%lld must be a multiple of 8 and <= 8192", who, (long long)a.H);
     if (a.M == 0 || a.H == 0) return H3FP8_OK;
     int rc = check_rows(a.x, a.ldx, a.H, gate ? "residual" : "x", who);
     if (!rc && gate) rc = check_rows(a.gate, a.ld_gate, a.H, "gate", who);
-    if (!rc && gate) rc = check_rows(a.branch, a.ld_branch, a.H, "branch", who);
-    if (!rc && gate) rc = check_rows(a.residual_out, a.ld_res, a.H, "residual_out", who);
-    if (!rc) rc = check_rows(a.weight, a.H, a.H, "weight", who);
-    if (!rc) rc = check_rows(a.shift, a.ld_shift, a.H, "shift", who);
-    if (!rc) rc = check_rows(a.scale, a.ld_scale, a.H, "scale", who);
+    if (!rc && gate && !b32) rc = check_rows(a.branch, a.ld_branch, a.H, "branch", who);
+    if (!rc && gate) rc = check_rows(a.residual_out, a.ld_res, a.H, gate && norm ? "residual_out" : "out", who);
+    if (!rc && norm) rc = check_rows(a.weight, a.H, a.H, "weight", who);
+    if (!rc && norm) rc = check_rows(a.shift, a.ld_shift, a.H, "shift", who);
+    if (!rc && norm) rc = check_rows(a.scale, a.ld_scale, a.H, "scale", who);
     if (!rc && a.h_out) rc = check_rows(a.h_out, a.ldh, a.H, "h_out", who);
     if (rc) return rc;
+    if (b32) {
+        H3_REQUIRE(a.acc && a.sa && a.sb && a.ld_acc >= a.H && a.ld_acc % 4 == 0 && ((uintptr_t)a.acc & 15) == 0 &&
+                       ((uintptr_t)a.sb & 15) == 0 && ((uintptr_t)a.bias & 15) == 0,
+                   "%s: the fp32 product rows and sb must be 16-byte aligned (row stride a multiple of 4 >= H), "
+                   "bias 16-byte aligned, sa / sb given", who);
+        H3_REQUIRE((uint64_t)a.H * 4 <= 0xffffffffull, "%s: row too wide", who);
+    }
     H3_REQUIRE(a.indices && a.idx_stride >= 0 && a.n_index > 0, "%s: bad indices or empty tables", who);
+    if (!norm) return H3FP8_OK;
     H3_REQUIRE(a.q || a.h_out, "%s: neither q nor h_out given", who);
     if (a.q)
         H3_REQUIRE(a.qscale && a.ldq >= a.H && a.ldq % 8 == 0 && ((uintptr_t)a.q & 7) == 0,
@@ -302,10 +360,10 @@ int check_rms(const RmsArgs& a, bool gate, const char* who) {
     return H3FP8_OK;
 }
 
-template <bool GATE>
+template <bool GATE, bool B32 = false>
 int launch_rms_out(const RmsArgs& a, hipStream_t st) {
-    if (!a.q) return launch_rms<GATE, 2>(a, st);
-    return a.h_out ? launch_rms<GATE, 3>(a, st) : launch_rms<GATE, 1>(a, st);
+    if (!a.q) return launch_rms<GATE, 2, B32>(a, st);
+    return a.h_out ? launch_rms<GATE, 3, B32>(a, st) : launch_rms<GATE, 1, B32>(a, st);
 }
 
 }  // namespace
@@ -326,7 +384,7 @@ int h3fp8_rms_quant(const void* x, int64_t ldx, const void* weight, const void* 
     a.q = (uint8_t*)q; a.ldq = ldq; a.qscale = qscale;
     a.h_out = (uint16_t*)h_out; a.ldh = ldh;
     H3_REQUIRE(idx_bytes == 4 || idx_bytes == 8, "h3fp8_rms_quant: indices must be int32 or int64");
-    int rc = check_rms(a, false, "h3fp8_rms_quant");
+    int rc = check_rms(a, false, false, true, "h3fp8_rms_quant");
     if (rc || M == 0 || H == 0) return rc;
     hipStream_t st = (hipStream_t)stream;
     return launch_rms_out<false>(a, st);
@@ -350,10 +408,51 @@ int h3fp8_gate_rms_quant(const void* residual, int64_t ldr, const void* gate, in
     a.q = (uint8_t*)q; a.ldq = ldq; a.qscale = qscale;
     a.h_out = (uint16_t*)h_out; a.ldh = ldh;
     H3_REQUIRE(idx_bytes == 4 || idx_bytes == 8, "h3fp8_gate_rms_quant: indices must be int32 or int64");
-    int rc = check_rms(a, true, "h3fp8_gate_rms_quant");
+    int rc = check_rms(a, true, false, true, "h3fp8_gate_rms_quant");
     if (rc || M == 0 || H == 0) return rc;
     hipStream_t st = (hipStream_t)stream;
     return launch_rms_out<true>(a, st);
+}
+
+int h3fp8_scale_gate_rms_quant(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                               const void* residual, int64_t ldr, const void* gate, int64_t ld_gate,
+                               const void* weight, const void* shift, int64_t ld_shift, const void* scale,
+                               int64_t ld_scale, int64_t n_index, const void* indices, int64_t idx_stride,
+                               int idx_bytes, int64_t M, int64_t H, float eps, void* residual_out, int64_t ld_res,
+                               void* q, int64_t ldq, float* qscale, void* h_out, int64_t ldh, void* stream) {
+    RmsArgs a{};
+    a.x = (const uint16_t*)residual; a.ldx = ldr;
+    a.gate = (const uint16_t*)gate; a.ld_gate = ld_gate;
+    a.acc = acc; a.ld_acc = ld_acc; a.sa = sa; a.sb = sb; a.bias = (const uint16_t*)bias;
+    a.residual_out = (uint16_t*)residual_out; a.ld_res = ld_res;
+    a.weight = (const uint16_t*)weight;
+    a.shift = (const uint16_t*)shift; a.ld_shift = ld_shift;
+    a.scale = (const uint16_t*)scale; a.ld_scale = ld_scale;
+    a.indices = indices; a.idx_stride = idx_stride; a.n_index = n_index; a.idx64 = idx_bytes == 8;
+    a.M = M; a.H = H; a.eps = eps;
+    a.q = (uint8_t*)q; a.ldq = ldq; a.qscale = qscale;
+    a.h_out = (uint16_t*)h_out; a.ldh = ldh;
+    H3_REQUIRE(idx_bytes == 4 || idx_bytes == 8, "h3fp8_scale_gate_rms_quant: indices must be int32 or int64");
+    int rc = check_rms(a, true, true, true, "h3fp8_scale_gate_rms_quant");
+    if (rc || M == 0 || H == 0) return rc;
+    return launch_rms_out<true, true>(a, (hipStream_t)stream);
+}
+
+int h3fp8_scale_indexed_gate(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                             const void* x, int64_t ldx, const void* gate, int64_t ld_gate, int64_t n_index,
+                             const void* indices, int64_t idx_stride, int idx_bytes, int64_t M, int64_t H, void* out,
+                             int64_t ldo, void* stream) {
+    RmsArgs a{};
+    a.x = (const uint16_t*)x; a.ldx = ldx;
+    a.gate = (const uint16_t*)gate; a.ld_gate = ld_gate;
+    a.acc = acc; a.ld_acc = ld_acc; a.sa = sa; a.sb = sb; a.bias = (const uint16_t*)bias;
+    a.residual_out = (uint16_t*)out; a.ld_res = ldo;
+    a.indices = indices; a.idx_stride = idx_stride; a.n_index = n_index; a.idx64 = idx_bytes == 8;
+    a.M = M; a.H = H;
+    H3_REQUIRE(idx_bytes == 4 || idx_bytes == 8, "h3fp8_scale_indexed_gate: indices must be int32 or int64");
+    int rc = check_rms(a, true, true, false, "h3fp8_scale_indexed_gate");
+    if (rc || M == 0 || H == 0) return rc;
+    return launch_rms<true, 0, true, false>(a, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -318,6 +318,96 @@ def gate_rms_quant(residual: torch.Tensor, gate: torch.Tensor, branch: torch.Ten
     return res, q, s
 
 
+# ---- consumers of a two-pass GEMM's fp32 product (the scale pass fused in) ----------------------------------------
+
+def _product_args(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None, M: int, N: int):
+    """The fp32 product [M, >= N] and contiguous sa [M] / sb [N] fp32 vectors (scalars broadcast), bias bf16 [N]."""
+    _need_cuda(x32, sa, sb, bias)
+    if x32.dtype != torch.float32 or x32.dim() != 2 or x32.shape[0] != M or x32.shape[1] < N:
+        raise ValueError(f"the product must be fp32 [{M}, >= {N}], got {x32.dtype} {tuple(x32.shape)}")
+    s_a = sa.reshape(-1).float()
+    s_a = (s_a.expand(M) if s_a.numel() == 1 else s_a).contiguous()
+    s_b = sb.reshape(-1).float()
+    s_b = (s_b.expand(x32.shape[1]) if s_b.numel() == 1 else s_b).contiguous()
+    if s_a.numel() != M or s_b.numel() < N:
+        raise ValueError("scale vectors do not match the product")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.dim() != 1 or bias.numel() < N
+                             or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous bf16 vector")
+    return s_a, s_b
+
+
+def scale_gate_rms_quant(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
+                         residual: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor,
+                         scale: torch.Tensor, indices: torch.Tensor, eps: float, residual_out: torch.Tensor | None = None,
+                         quant: bool = False, modulated: bool = True):
+    """``indexed_gate_rms_norm_scale_shift(residual, gate, branch, ...)`` with branch = the scale pass of the fp32
+    product ``x32`` (h3_tp2/fp8_consumers.py:464-485): (residual_out, modulated bf16) and, with ``quant``, the per-token
+    e4m3 quant of the modulated row as well: (residual_out, q, scale[, modulated])."""
+    M, H, n_index, ib = _producer_args(residual, weight, (gate, shift, scale), indices, ("gate", "shift", "scale"))
+    s_a, s_b = _product_args(x32, sa, sb, bias, M, H)
+    res = residual_out if residual_out is not None else torch.empty((M, H), device=residual.device,
+                                                                    dtype=torch.bfloat16)
+    h = torch.empty((M, H), device=residual.device, dtype=torch.bfloat16) if modulated or not quant else None
+    q = torch.empty((M, H), device=residual.device, dtype=E4M3) if quant else None
+    s = torch.empty((M, 1), device=residual.device, dtype=torch.float32) if quant else None
+    _lib.call("h3fp8_scale_gate_rms_quant", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), s_b.data_ptr(),
+              bias.data_ptr() if bias is not None else None, residual.data_ptr(), _rows(residual, "residual"),
+              gate.data_ptr(), _rows(gate, "gate"), weight.data_ptr(), shift.data_ptr(), _rows(shift, "shift"),
+              scale.data_ptr(), _rows(scale, "scale"), n_index, indices.data_ptr(), indices.stride(0), ib, M, H,
+              float(eps), res.data_ptr(), _rows(res, "residual_out"), q.data_ptr() if q is not None else None,
+              H, s.data_ptr() if s is not None else None, h.data_ptr() if h is not None else None, H,
+              _stream(residual))
+    if quant:
+        return (res, q, s, h) if h is not None else (res, q, s)
+    return res, h
+
+
+def scale_indexed_gate(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
+                       x: torch.Tensor, gate: torch.Tensor, indices: torch.Tensor,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """``indexed_gate(x, gate, other, indices)`` = bf16(x + gate[indices] * other) with other = the scale pass of the
+    fp32 product ``x32`` (h3_tp2/fp8_consumers.py:488-504)."""
+    _need_cuda(x, gate, indices)
+    M, H = x.shape
+    if x.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or gate.dim() != 2 or gate.shape[1] != H:
+        raise ValueError("x and gate must be bf16 with the same width")
+    if indices.dim() != 1 or indices.shape[0] != M or indices.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"indices must be int32/int64 [{M}]")
+    s_a, s_b = _product_args(x32, sa, sb, bias, M, H)
+    o = out if out is not None else torch.empty((M, H), device=x.device, dtype=torch.bfloat16)
+    _lib.call("h3fp8_scale_indexed_gate", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), s_b.data_ptr(),
+              bias.data_ptr() if bias is not None else None, x.data_ptr(), _rows(x, "x"), gate.data_ptr(),
+              _rows(gate, "gate"), gate.shape[0], indices.data_ptr(), indices.stride(0), indices.element_size(), M, H,
+              o.data_ptr(), _rows(o, "out"), _stream(x))
+    return o
+
+
+def scale_qk_norm_rope(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
+                       num_heads: int, num_kv_heads: int, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                       rope_table: torch.Tensor, eps: float):
+    """q, k of ``fused_qk_norm_rope`` (head_dim 128, rotary 96, half-split) on the qkv GEMM's fp32 product: the q heads
+    are product columns [0, 128 H), the k heads the next 128 Hk.  Returns (q [T, H, 128], k [T, Hk, 128]) bf16
+    (h3_tp2/fp8_consumers.py:424-461 without the v pass)."""
+    T = x32.shape[0]
+    s_a, s_b = _product_args(x32, sa, sb, bias, T, (num_heads + num_kv_heads) * 128)
+    _need_cuda(q_weight, k_weight, rope_table)
+    if rope_table.dim() != 2 or rope_table.shape != (T, 96) or rope_table.stride(1) != 1 \
+            or rope_table.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"rope_table must be fp32/bf16 [{T}, 96] with contiguous rows")
+    for w in (q_weight, k_weight):
+        if w.dtype != torch.bfloat16 or w.numel() != 128 or not w.is_contiguous():
+            raise ValueError("q/k norm weights must be contiguous bf16 [128]")
+    oq = torch.empty((T, num_heads, 128), device=x32.device, dtype=torch.bfloat16)
+    ok = torch.empty((T, num_kv_heads, 128), device=x32.device, dtype=torch.bfloat16)
+    _lib.call("h3fp8_scale_qk_norm_rope", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), s_b.data_ptr(),
+              bias.data_ptr() if bias is not None else None, T, num_heads, num_kv_heads, q_weight.data_ptr(),
+              k_weight.data_ptr(), rope_table.data_ptr(), rope_table.stride(0) if T > 1 else 96,
+              int(rope_table.dtype == torch.float32), float(eps), oq.data_ptr(), oq.stride(0), oq.stride(1),
+              ok.data_ptr(), ok.stride(0), ok.stride(1), _stream(x32))
+    return oq, ok
+
+
 def scale_bias_cast(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
                     out_dtype: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:
     """The two-pass scale pass: round(sa * (sb * x32)) (+ bias by one fma) (h3_tp2/fp8_gemm.py:37-54, :167-171)."""

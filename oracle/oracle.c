@@ -342,3 +342,65 @@ void oracle_gate_rms_quant(const uint16_t* residual, int64_t ldr, const uint16_t
         qscale[m] = oracle_quant_row_f32(xf, H, q + m * H);
     }
 }
+
+/* ---- consumers of the GEMM output (h3_tp2/fp8_consumers.py:131-293) ------------------------------------------------
+ *
+ * fused_qk_norm_rope's half-split path on one bf16 head of 128 dims (the stock `_rms_norm_rope_kernel` as the
+ * reference's CPU stand-in states it, tests/fake_h3_consumers.py:29-48), rotary_half = 48:
+ *   var = fp32(sum_d x_d * x_d) / 128;  r = 1 / sqrt(var + eps)
+ *   n_d = bf16((x_d * r) * w_d)
+ *   pair(d) = d + 48 (d < 48), d - 48 (48 <= d < 96), d;  freq(d) = d (d < 48), d - 48 (48 <= d < 96), 0
+ *   c = table[freq(d)], s = table[freq(d) + 48]
+ *   out_d = bf16(n_d * c - n_pair * s) (d < 48), bf16(n_d * c + n_pair * s) (48 <= d < 96), n_d (d >= 96)
+ * The sum of squares is rounded once to fp32 from an fp64 sum in the HIP kernel's order: lane l adds the squares of
+ * dims 2l and 2l + 1, then an xor butterfly over the 64 lane sums (distances 32, ..., 1). */
+static double head_sumsq(const float* x) {
+    double p[64];
+    for (int l = 0; l < 64; ++l) {
+        double s = 0.0;
+        s += (double)(x[2 * l] * x[2 * l]);
+        s += (double)(x[2 * l + 1] * x[2 * l + 1]);
+        p[l] = s;
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        double t[64];
+        for (int l = 0; l < 64; ++l) t[l] = p[l] + p[l ^ d];
+        memcpy(p, t, sizeof(p));
+    }
+    return p[0];
+}
+
+/* x: bf16 bits [T, heads, 128] (contiguous), weight [128] bf16 bits, table: fp32 [T, 96] (the rope table's values),
+ * out: bf16 bits [T, heads, 128]. */
+void oracle_qk_norm_rope(const uint16_t* x, int64_t T, int64_t heads, const uint16_t* weight, const float* table,
+                         float eps, uint16_t* out) {
+    float xf[128];
+    uint16_t n[128];
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t h = 0; h < heads; ++h) {
+            const uint16_t* xr = x + (t * heads + h) * 128;
+            for (int d = 0; d < 128; ++d) xf[d] = oracle_bf16_to_f32(xr[d]);
+            volatile float var = (float)head_sumsq(xf);
+            volatile float hd = 128.0f;
+            var = var / hd;
+            volatile float dd = sqrtf(var + eps);
+            volatile float one = 1.0f;
+            const float r = one / dd;
+            for (int d = 0; d < 128; ++d) {
+                volatile float v = xf[d] * r;
+                v = v * oracle_bf16_to_f32(weight[d]);
+                n[d] = oracle_bf16_rne(v);
+            }
+            const float* tb = table + t * 96;
+            uint16_t* o = out + (t * heads + h) * 128;
+            for (int d = 0; d < 128; ++d) {
+                if (d >= 96) { o[d] = n[d]; continue; }
+                const int pd = d < 48 ? d + 48 : d - 48, fd = d < 48 ? d : d - 48;
+                const float c = tb[fd], s = tb[fd + 48];
+                volatile float a = oracle_bf16_to_f32(n[d]) * c;
+                volatile float b = oracle_bf16_to_f32(n[pd]) * s;
+                volatile float y = d < 48 ? a - b : a + b;
+                o[d] = oracle_bf16_rne(y);
+            }
+        }
+}

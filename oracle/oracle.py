@@ -21,6 +21,9 @@ Each function names the reference code it restates (paths relative to the refere
 * ``gate_rms_quant``      h3_tp2/fp8_quant_fuse.py:191-243, :349-369: ``indexed_gate_rms_norm_scale_shift``
                           (tests/fake_h3_consumers.py:66-74), then ``quant_rows``
 * ``row_sumsq``           the sum of squares of those producers, in fp64, in the HIP kernel's fixed order
+* ``qk_norm_rope``        the stock ``fused_qk_norm_rope`` half-split kernel as tests/fake_h3_consumers.py:29-48 states
+                          it (head_dim 128, rotary 96); the fused consumer of h3_tp2/fp8_consumers.py:131-193 is
+                          ``epilogue`` (the scale pass) followed by it
 
 Pinning (what each function is checked against, in tests/test_oracle.py): the e4m3fn/bf16/fp16 casts against torch's
 and numpy's own casts on exhaustive or dense sweeps; ``quant_rows`` against known answers of the reference's tests
@@ -75,6 +78,7 @@ def lib() -> ctypes.CDLL:
         F = ctypes.c_float
         L.oracle_rms_quant.argtypes = [P, I64, P, P, I64, P, I64, P, I64, I64, F, P, P, P]
         L.oracle_gate_rms_quant.argtypes = [P, I64, P, I64, P, I64, P, P, I64, P, I64, P, I64, I64, F, P, P, P, P]
+        L.oracle_qk_norm_rope.argtypes = [P, I64, I64, P, P, F, P]
         L.oracle_e4m3fn_from_f32.argtypes = [ctypes.c_float]
         L.oracle_e4m3fn_from_f32.restype = ctypes.c_uint8
         L.oracle_bf16_rne.argtypes = [ctypes.c_float]
@@ -301,3 +305,17 @@ def gate_rms_quant(residual_bits, gate_bits, branch_bits, weight_bits, shift_bit
     lib().oracle_gate_rms_quant(_p(r), H, _p(g), ldg, _p(br), H, _p(w), _p(sh), ldsh, _p(sc), ldsc, _p(idx), M, H,
                                 float(eps), _p(ro), _p(h), _p(q), _p(s))
     return ro, h, q, s
+
+
+def qk_norm_rope(x_bits: np.ndarray, weight_bits: np.ndarray, table: np.ndarray, eps: float) -> np.ndarray:
+    """bf16 heads [T, heads, 128] (bit patterns), norm weight [128], rope table [T, 96] (its fp32 values: cos | sin)
+    -> bf16 bits [T, heads, 128]."""
+    x = _u16(x_bits)
+    T, heads, D = x.shape
+    assert D == 128
+    w = _u16(weight_bits).reshape(-1)
+    tb = np.ascontiguousarray(table, dtype=np.float32)
+    assert w.size == 128 and tb.shape == (T, 96)
+    out = np.empty_like(x)
+    lib().oracle_qk_norm_rope(_p(x), T, heads, _p(w), _p(tb), float(eps), _p(out))
+    return out

@@ -179,3 +179,33 @@ def standin_gate_rms(residual, gate, branch, weight, shift, scale, idx, eps):
     """The stock indexed_gate_rms_norm_scale_shift as the CPU stand-in evaluates it (fake_h3_consumers.py:66-74)."""
     upd = (residual.float() + gate.index_select(0, idx).float() * branch.float()).to(torch.bfloat16)
     return upd, standin_rms(upd, weight, shift, scale, idx, eps)
+
+
+def standin_qk_norm_rope(x, weight, table, eps):
+    """The stock fused_qk_norm_rope half-split kernel as the reference's CPU stand-in evaluates it (torch CPU ops,
+    tests/fake_h3_consumers.py:29-48): bf16 [T, H, 128] -> bf16 [T, H, 128]; table [T, 96] (cos | sin)."""
+    T, Hh, D = x.shape
+    half = table.shape[-1] // 2
+    rot = 2 * half
+    dims = torch.arange(D)
+    xf = x.float()
+    w = weight.float()
+    inv = torch.rsqrt((xf * xf).sum(dim=-1) / D + eps)
+    n = (xf * inv[..., None] * w).to(torch.bfloat16)
+    pd = torch.where(dims < half, dims + half, torch.where(dims < rot, dims - half, dims))
+    p = (xf[..., pd] * inv[..., None] * w[pd]).to(torch.bfloat16)
+    fd = torch.where(dims < half, dims, torch.where(dims < rot, dims - half, torch.zeros_like(dims)))
+    cos = table[:, fd].float()[:, None, :]
+    sin = table[:, fd + half].float()[:, None, :]
+    first = n.float() * cos - p.float() * sin
+    second = n.float() * cos + p.float() * sin
+    out = torch.where(dims < rot, torch.where(dims < half, first, second), n.float())
+    return out.to(x.dtype)
+
+
+def rope_table(T: int, dtype, seed: int = 3):
+    """A rope table [T, 96] = cos | sin of seeded positions times 48 frequencies (the reference's
+    tests/test_fp8_consumer_fuse.py:64-67 generator)."""
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand(T, 1, generator=g) * 500 * torch.exp(-torch.arange(48) / 8.0)[None, :]
+    return torch.cat((torch.cos(pos), torch.sin(pos)), dim=-1).to(dtype)

@@ -1,0 +1,239 @@
+"""The consumers of a two-pass GEMM's fp32 product with the scale pass fused in (qk-RMSNorm + RoPE of the qkv output,
+the gated residual + RMS/AdaLN of the out projection's output, indexed_gate of the fc2 output) against the oracle:
+the scale pass (oracle ``epilogue``) followed by the stock consumer's arithmetic, bit for bit.
+
+Follows the reference's tests/test_fp8_consumer_fuse.py:47-167 (operands with accumulators in the thousands and
+log-uniform scales, GQA-style head counts, biases, rope tables in fp32 and bf16, odd row counts, a hidden size that is
+not a power of two, [U, 6H] chunk-view modulation tables, directed values pushed to inf by the scales) and its
+block-level protocol tests (the stash consumed by the fused consumer after the self-check).
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_quant_equal, bits16, mod_inputs, rope_table
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+EPS = 1e-6
+
+
+def _operands(T, N, seed, *, bias=False, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x32 = torch.randn(T, N, generator=g) * 3000 * scale
+    sa = torch.exp(torch.empty(T).uniform_(-9.0, -2.0, generator=g))
+    sb = torch.exp(torch.empty(N).uniform_(-9.5, -7.5, generator=g))
+    b = (torch.randn(N, generator=g) * 0.1).to(BF16) if bias else None
+    return x32, sa, sb, b
+
+
+def _nan_aware_equal(out_bits, ref_bits, what):
+    nan_ref = (ref_bits & 0x7FFF) > 0x7F80
+    assert np.array_equal((out_bits & 0x7FFF) > 0x7F80, nan_ref), f"{what}: NaN positions differ"
+    bad = (out_bits != ref_bits) & ~nan_ref
+    assert not bad.any(), f"{what}: {int(bad.sum())} values differ, first at {np.argwhere(bad)[:5].tolist()}"
+
+
+def _epi(x32, sa, sb, b):
+    return O.epilogue(x32.numpy(), sa.numpy(), sb.numpy(), None if b is None else bits16(b))
+
+
+def _dev(*ts, cuda):
+    return [None if t is None else t.to(cuda) for t in ts]
+
+
+@pytest.mark.parametrize("T", [1, 37, 300])
+@pytest.mark.parametrize("H,Hk", [(2, 2), (3, 1), (24, 8)])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("rope_dtype", [torch.bfloat16, torch.float32])
+def test_qk_norm_rope_matches_oracle(cuda, T, H, Hk, bias, rope_dtype):
+    from h3_tp2_amd import fp8_consumers as fc
+    D = 128
+    N = (H + 2 * Hk) * D
+    x32, sa, sb, b = _operands(T, N, seed=T * 7 + H, bias=bias)
+    g = torch.Generator().manual_seed(5)
+    wq = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    wk = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    rope = rope_table(T, rope_dtype)
+    x32d, sad, sbd, bd, wqd, wkd, roped = _dev(x32, sa, sb, b, wq, wk, rope, cuda=cuda)
+    st = fc.Stash(x32d, sad, sbd, bd, torch.empty((T, N), dtype=BF16, device=cuda))
+    oq, ok, v = fc.qk_norm_rope_fused(st, H, Hk, D, wqd, wkd, roped, EPS)
+    torch.cuda.synchronize()
+    p = _epi(x32, sa, sb, b)                                      # the scale pass: bf16 qkv
+    tab = rope.float().numpy()
+    rq = O.qk_norm_rope(p[:, :H * D].reshape(T, H, D), bits16(wq), tab, EPS)
+    rk = O.qk_norm_rope(p[:, H * D:(H + Hk) * D].reshape(T, Hk, D), bits16(wk), tab, EPS)
+    _nan_aware_equal(bits16(oq), rq, "q")
+    _nan_aware_equal(bits16(ok), rk, "k")
+    assert np.array_equal(bits16(v), p[:, (H + Hk) * D:].reshape(T, Hk, D))
+    assert v.data_ptr() == st.ph.data_ptr() + (H + Hk) * D * 2
+
+
+@pytest.mark.parametrize("T,hidden", [(1, 128), (37, 200), (64, 256), (1000, 3072), (300, 5376)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_gate_rms_matches_oracle(cuda, T, hidden, bias):
+    from h3_tp2_amd import fp8_consumers as fc, ops
+    x32, sa, sb, b = _operands(T, hidden, seed=T + hidden, bias=bias)
+    res, w, sh, sc, gt, idx = mod_inputs(T, hidden, seed=T + 2 * hidden, B=3)
+    branch = _epi(x32, sa, sb, b)
+    r_ref, h_ref, q_ref, s_ref = O.gate_rms_quant(bits16(res), bits16(gt), branch, bits16(w), bits16(sh), bits16(sc),
+                                                  idx.numpy(), EPS)
+    base = sh._base.to(cuda)
+    shd, scd, gd = base[:, :hidden], base[:, hidden:2 * hidden], base[:, 2 * hidden:3 * hidden]
+    x32d, sad, sbd, bd = _dev(x32, sa, sb, b, cuda=cuda)
+    st = fc.Stash(x32d, sad, sbd, bd, torch.empty((T, hidden), dtype=BF16, device=cuda))
+    f_res, f_mod = fc.gate_rms_fused(st, res.to(cuda), gd, w.to(cuda), shd, scd, idx.to(cuda), EPS)
+    torch.cuda.synchronize()
+    assert f_res.data_ptr() == st.ph.data_ptr()
+    _nan_aware_equal(bits16(f_res), r_ref, "residual_out")
+    _nan_aware_equal(bits16(f_mod), h_ref, "modulated")
+    # the out-projection consumer and the fc1 input's quant in one pass
+    r2, q2, s2 = ops.scale_gate_rms_quant(x32d, sad, sbd, bd, res.to(cuda), gd, w.to(cuda), shd, scd,
+                                          idx.to(torch.int32).to(cuda), EPS, quant=True, modulated=False)
+    torch.cuda.synchronize()
+    _nan_aware_equal(bits16(r2), r_ref, "residual_out (quant form)")
+    assert_quant_equal(q2, s2, q_ref, s_ref)
+
+
+@pytest.mark.parametrize("T,hidden", [(1, 128), (37, 200), (2000, 3072)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_indexed_gate_matches_oracle(cuda, T, hidden, bias):
+    from h3_tp2_amd import fp8_consumers as fc
+    x32, sa, sb, b = _operands(T, hidden, seed=3 * T + hidden, bias=bias)
+    x, w, sh, sc, gt, idx = mod_inputs(T, hidden, seed=T + 5, B=2)
+    branch = _epi(x32, sa, sb, b)
+    r_ref, _, _, _ = O.gate_rms_quant(bits16(x), bits16(gt), branch, bits16(w), bits16(sh), bits16(sc), idx.numpy(),
+                                      EPS)
+    gd = gt._base.to(cuda)[:, 2 * hidden:3 * hidden]
+    x32d, sad, sbd, bd = _dev(x32, sa, sb, b, cuda=cuda)
+    st = fc.Stash(x32d, sad, sbd, bd, torch.empty((T, hidden), dtype=BF16, device=cuda))
+    out = fc.gate_fused(st, x.to(cuda), gd, idx.to(cuda))
+    torch.cuda.synchronize()
+    assert out.data_ptr() == st.ph.data_ptr()
+    _nan_aware_equal(bits16(out), r_ref, "indexed_gate")
+
+
+def test_directed_values_all_consumers(cuda):
+    """Midpoints, subnormals, +-0, products pushed to inf by the scales, NaN: still the oracle's bits (NaN positions
+    compared as positions)."""
+    from h3_tp2_amd import fp8_consumers as fc
+    T, H, D = 5, 2, 128
+    N = 3 * H * D
+    vals = torch.tensor([0.0, -0.0, 1e-40, -1e-40, 1.0, -1.0, 3e38, -3e38, 1e4, -1e4, 0.5000001, 1.9999999,
+                         float("inf"), -float("inf"), float("nan")])
+    x32 = vals.repeat(T, N // vals.numel() + 1)[:, :N].clone()
+    x32 = torch.roll(x32, shifts=1, dims=1)
+    x32[1:] = torch.randn(T - 1, N) * 1e3
+    x32[2, 7] = float("nan")
+    sa = torch.tensor([1.0, 2.0 ** -7, 3.0, 1e-3, 1.0])
+    sb = torch.ones(N)
+    sb[::3] = 2.0 ** 100
+    w = torch.ones(D, dtype=BF16)
+    rope = rope_table(T, BF16)
+    st = fc.Stash(*_dev(x32, sa, sb, None, cuda=cuda), torch.empty((T, N), dtype=BF16, device=cuda))
+    oq, ok, v = fc.qk_norm_rope_fused(st, H, H, D, w.to(cuda), w.to(cuda), rope.to(cuda), EPS)
+    torch.cuda.synchronize()
+    p = _epi(x32, sa, sb, None)
+    tab = rope.float().numpy()
+    _nan_aware_equal(bits16(oq), O.qk_norm_rope(p[:, :H * D].reshape(T, H, D), bits16(w), tab, EPS), "q")
+    _nan_aware_equal(bits16(ok), O.qk_norm_rope(p[:, H * D:2 * H * D].reshape(T, H, D), bits16(w), tab, EPS), "k")
+    _nan_aware_equal(bits16(v), p[:, 2 * H * D:].reshape(T, H, D), "v")
+
+    hid = 200
+    x32 = vals.repeat(T, hid // vals.numel() + 1)[:, :hid].clone()
+    sa, sb = torch.ones(T), torch.ones(hid)
+    res = torch.randn(T, hid, generator=torch.Generator().manual_seed(1)).to(BF16)
+    g6 = torch.randn(1, 6 * hid, generator=torch.Generator().manual_seed(2)).to(BF16)
+    idx = torch.zeros(T, dtype=torch.long)
+    branch = _epi(x32, sa, sb, None)
+    wn = torch.ones(hid, dtype=BF16)
+    r_ref, h_ref, _, _ = O.gate_rms_quant(bits16(res), bits16(g6[:, 2 * hid:3 * hid]), branch, bits16(wn),
+                                          bits16(g6[:, 3 * hid:4 * hid]), bits16(g6[:, 4 * hid:5 * hid]), idx.numpy(),
+                                          EPS)
+    g6d = g6.to(cuda)
+    st = fc.Stash(*_dev(x32, sa, sb, None, cuda=cuda), torch.empty((T, hid), dtype=BF16, device=cuda))
+    f_res, f_mod = fc.gate_rms_fused(st, res.to(cuda), g6d[:, 2 * hid:3 * hid], wn.to(cuda), g6d[:, 3 * hid:4 * hid],
+                                     g6d[:, 4 * hid:5 * hid], idx.to(cuda), EPS)
+    torch.cuda.synchronize()
+    _nan_aware_equal(bits16(f_res), r_ref, "residual_out")
+    _nan_aware_equal(bits16(f_mod), h_ref, "modulated")
+
+
+def test_consumer_wrappers_take_the_stash_after_the_selfcheck(cuda, monkeypatch):
+    """The wrapped consumers with the fused kernels registered: a pending stash is consumed by the fused consumer once
+    its self-check against the scale pass + the stock consumer passes (stock consumers here with the same arithmetic:
+    the producer kernel on a bf16 branch, torch's elementwise indexed_gate, the qk kernel on the bf16 values); the
+    results equal the stock path's."""
+    import threading
+
+    from h3_tp2_amd import fp8_consumers as fc, ops
+
+    st_state = dict(fc._state)
+    st_state["checked"], st_state["disabled"], st_state["fused"] = {}, set(), {}
+    monkeypatch.setattr(fc, "_state", st_state)
+    monkeypatch.setattr(fc, "_stats", dict.fromkeys(fc._stats, 0))
+    monkeypatch.setattr(fc, "_tls", threading.local())
+
+    def stock_gate_rms(residual, gate, branch, weight, shift, scale, indices, eps):
+        return ops.indexed_gate_rms_norm_scale_shift(residual, gate, branch, weight, shift, scale, indices, eps)
+
+    def stock_gate(x, gate, other, indices):
+        return (x.float() + gate.index_select(0, indices).float() * other.float()).to(x.dtype)
+
+    def stock_qk(q, k, q_weight, k_weight, rope, eps, *, head_dim=None, rotary_dim=None, interleaved=False):
+        T, H, D = q.shape
+        Hk = k.shape[1]
+        flat = torch.cat([q.reshape(T, H * D), k.reshape(T, Hk * D)], dim=1).float().contiguous()
+        ones_a = torch.ones(T, device=q.device)
+        ones_b = torch.ones(flat.shape[1], device=q.device)
+        return ops.scale_qk_norm_rope(flat, ones_a, ones_b, None, H, Hk, q_weight, k_weight, rope, eps)
+
+    wrapped = {"out": fc.make_consumer_wrapper("out", stock_gate_rms), "fc2": fc.make_consumer_wrapper("fc2", stock_gate),
+               "qkv": fc.make_consumer_wrapper("qkv", stock_qk)}
+    fc.set_fused("out", fc.make_fused_gate_rms(stock_gate_rms))
+    fc.set_fused("fc2", fc.make_fused_gate(stock_gate))
+    fc.set_fused("qkv", fc.make_fused_qk(stock_qk))
+    T, hidden = 300, 3072
+    res, w, sh, sc, gt, idx = mod_inputs(T, hidden, seed=31, B=3)
+    base = sh._base.to(cuda)
+    shd, scd, gd = base[:, :hidden], base[:, hidden:2 * hidden], base[:, 2 * hidden:3 * hidden]
+    resd, wd, idxd = res.to(cuda), w.to(cuda), idx.to(cuda)
+    ctx = fc._Ctx({})
+    fc._tls.ctx = ctx
+    try:
+        for site in ("out", "fc2"):
+            x32, sa, sb, b = _operands(T, hidden, seed=40 + len(site), bias=site == "out")
+            st = fc.Stash(*_dev(x32, sa, sb, b, cuda=cuda), torch.empty((T, hidden), dtype=BF16, device=cuda))
+            ref_branch = st.rows(T).materialize()                       # the stock path's bf16 branch
+            ctx.pending[site] = st
+            if site == "out":
+                got = wrapped["out"](resd, gd, st.ph, wd, shd, scd, idxd, EPS)
+                want = stock_gate_rms(resd, gd, ref_branch, wd, shd, scd, idxd, EPS)
+            else:
+                got = (wrapped["fc2"](resd, gd, st.ph, idxd),)
+                want = (stock_gate(resd, gd, ref_branch, idxd),)
+            assert not ctx.pending
+            for a, bb in zip(got, want):
+                assert torch.equal(a.view(torch.int16), bb.view(torch.int16)), site
+        D, H, Hk = 128, 4, 2
+        N = (H + 2 * Hk) * D
+        x32, sa, sb, b = _operands(T, N, seed=50, bias=True)
+        st = fc.Stash(*_dev(x32, sa, sb, b, cuda=cuda), torch.empty((T, N), dtype=BF16, device=cuda))
+        ref = st.rows(T).materialize()
+        wq = (1 + 0.1 * torch.randn(D, generator=torch.Generator().manual_seed(8))).to(BF16).to(cuda)
+        rope = rope_table(T, torch.float32).to(cuda)
+        ctx.pending["qkv"] = st
+        ph = st.ph
+        oq, ok = wrapped["qkv"](ph[:, :H * D].view(T, H, D), ph[:, H * D:(H + Hk) * D].view(T, Hk, D), wq, wq, rope,
+                                EPS)
+        rq, rk = stock_qk(ref[:, :H * D].view(T, H, D), ref[:, H * D:(H + Hk) * D].view(T, Hk, D), wq, wq, rope, EPS)
+        torch.cuda.synchronize()
+        assert torch.equal(oq.view(torch.int16), rq.view(torch.int16))
+        assert torch.equal(ok.view(torch.int16), rk.view(torch.int16))
+        assert torch.equal(ph[:, (H + Hk) * D:].view(torch.int16), ref[:, (H + Hk) * D:].view(torch.int16))
+    finally:
+        fc._tls.ctx = None
+    s = fc.stats()
+    assert (s["fused_out"], s["fused_fc2"], s["fused_qkv"], s["selfcheck_fail"]) == (1, 1, 1, 0), s
+    assert s["selfcheck_pass"] == 3 and s["materialize"] == 0

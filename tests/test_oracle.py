@@ -451,3 +451,69 @@ def test_rms_nonfinite_rows():
     nz = (shift2 & 0x7FFF) != 0
     assert np.array_equal(h[2][keep & nz], shift2[keep & nz])
     assert np.isfinite(s[[0, 3]]).all()
+
+
+# ---- the consumer of the qkv output: qk-RMSNorm + RoPE (head_dim 128, rotary 96) --------------------------------------
+
+from _util import rope_table, standin_qk_norm_rope  # noqa: E402
+
+
+def _heads(T, Hh, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    mag = torch.exp(torch.randn(T, Hh, 1, generator=g))
+    return (torch.randn(T, Hh, 128, generator=g) * mag * scale).to(BF16)
+
+
+def test_qk_norm_rope_rotation_closed_forms():
+    """cos = 1, sin = 0 passes the normalised row through; cos = 0, sin = 1 rotates it by a quarter turn:
+    out[d] = -n[d + 48] (d < 48), n[d - 48] (48 <= d < 96), n[d] (d >= 96).  A constant head of a power of two with
+    eps = 0 and weight 1 normalises to exactly +-1."""
+    T, Hh = 5, 3
+    x = _heads(T, Hh, seed=1)
+    w = (1.0 + 0.1 * torch.randn(128, generator=torch.Generator().manual_seed(2))).to(BF16)
+    ident = np.concatenate([np.ones((T, 48)), np.zeros((T, 48))], axis=1).astype(np.float32)
+    quarter = np.concatenate([np.zeros((T, 48)), np.ones((T, 48))], axis=1).astype(np.float32)
+    n = O.qk_norm_rope(bits16(x), bits16(w), ident, 1e-6)
+    r = O.qk_norm_rope(bits16(x), bits16(w), quarter, 1e-6)
+    want = n.copy()
+    want[..., :48] = n[..., 48:96] ^ 0x8000
+    want[..., 48:96] = n[..., :48]
+    assert np.array_equal(r, want)
+    c = torch.full((T, Hh, 128), -0.25).to(BF16)
+    c[1] = 8.0
+    out = O.qk_norm_rope(bits16(c), _bf(np.ones(128)), ident, 0.0)
+    assert np.array_equal(out[0], np.full((Hh, 128), 0xBF80, np.uint16)) and (out[1] == 0x3F80).all()
+
+
+def test_qk_norm_rope_scale_invariance():
+    """eps = 0: a head scaled by 2^k normalises to the same bf16 values, so the rotated output does not change."""
+    T, Hh = 4, 2
+    x = _heads(T, Hh, seed=3)
+    w = (1.0 + 0.1 * torch.randn(128, generator=torch.Generator().manual_seed(4))).to(BF16)
+    tab = rope_table(T, torch.float32).numpy()
+    base = O.qk_norm_rope(bits16(x), bits16(w), tab, 0.0)
+    for k in (-12, 7):
+        assert np.array_equal(O.qk_norm_rope(bits16((x.float() * 2.0 ** k).to(BF16)), bits16(w), tab, 0.0), base)
+
+
+@pytest.mark.parametrize("rope_dtype", [torch.float32, torch.bfloat16])
+def test_qk_norm_rope_matches_the_torch_standin(rope_dtype):
+    """torch's CPU evaluation of the stock kernel's stand-in: heads whose fp32 sums of squares agree are bit-identical
+    (every other operation is the same fp32 arithmetic); the others within one bf16 ulp plus 2^-20 of the rotated
+    terms."""
+    T, Hh = 64, 6
+    x = _heads(T, Hh, seed=5)
+    w = (1.0 + 0.1 * torch.randn(128, generator=torch.Generator().manual_seed(6))).to(BF16)
+    tab = rope_table(T, rope_dtype)
+    out = O.qk_norm_rope(bits16(x), bits16(w), tab.float().numpy(), 1e-6)
+    ref = bits16(standin_qk_norm_rope(x, w, tab, 1e-6))
+    xf = x.float()
+    torch_ss = (xf * xf).sum(dim=-1).numpy()
+    ours = np.array([[np.float32(O.row_sumsq(bits16(x[t, h]))) for h in range(Hh)] for t in range(T)])
+    same = torch_ss.view(np.uint32) == ours.view(np.uint32)
+    assert same.mean() > 0.5
+    assert np.array_equal(out[same], ref[same])
+    a, b = O.bf16_to_f32(out).astype(np.float64), O.bf16_to_f32(ref).astype(np.float64)
+    big = np.abs(O.bf16_to_f32(out)).max(axis=-1, keepdims=True) * 3
+    tol = np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + big * 2.0 ** -7
+    assert (np.abs(a - b) <= tol)[~same].all()
