@@ -270,6 +270,48 @@ def main() -> None:
                 del br
         out["producers_fused_quant"] = res
 
+    if want("consumers"):
+        # The consumers of the two-pass GEMM's fp32 product with the scale pass fused in: qk-RMSNorm + RoPE of the
+        # QKV output (960x576 5 s, 24 q + 24 k heads of 128, plus the v columns' scale pass), the gated residual +
+        # RMS/AdaLN of the out projection and indexed_gate of fc2 (1344x768 5 s, H = 3072).
+        from h3_tp2_amd import fp8_consumers as fc
+        gen = torch.Generator(device=dev).manual_seed(9)
+        res = {}
+        T, Hq = M, K // 128
+        x32 = torch.randn(T, N, device=dev, generator=gen) * 3000
+        sa_t = torch.rand(T, device=dev, generator=gen) * 1e-3 + 1e-4
+        sb_t = torch.rand(N, device=dev, generator=gen) * 1e-3 + 1e-4
+        wq = (1 + 0.1 * torch.randn(128, device=dev, generator=gen)).to(torch.bfloat16)
+        pos = torch.rand(T, 1, device=dev, generator=gen) * 500 * torch.exp(-torch.arange(48, device=dev) / 8.0)
+        rope = torch.cat((torch.cos(pos), torch.sin(pos)), dim=-1)
+        st = fc.Stash(x32, sa_t, sb_t, None, torch.empty((T, N), device=dev, dtype=torch.bfloat16))
+        t_qk = time_steps(lambda: fc.qk_norm_rope_fused(st, Hq, Hq, 128, wq, wq, rope, 1e-6), steps, warm) / steps
+        qk_bytes = T * N * 4.0 + T * N * 2.0                         # product in, q / k / v bf16 out
+        res["qkv_qk_norm_rope_16740x9216"] = {"ms": round(t_qk, 4), "GB/s": round(qk_bytes / (t_qk * 1e-3) / 1e9, 1),
+                                              "frac_hbm": round(qk_bytes / (t_qk * 1e-3) / 1e9 / PEAK_GBS, 4)}
+        del x32, st
+        Mc, H = synthetic.CONFIGS["c3_ffn_1344x768_5s"]["M"], K
+        x32 = torch.randn(Mc, H, device=dev, generator=gen) * 3000
+        sa_c = torch.rand(Mc, device=dev, generator=gen) * 1e-3 + 1e-4
+        sb_c = torch.rand(H, device=dev, generator=gen) * 1e-3 + 1e-4
+        resid = torch.randn(Mc, H, device=dev, generator=gen).to(torch.bfloat16)
+        wn = (1.0 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16)
+        ada = torch.randn(6, 6 * H, device=dev, generator=gen).to(torch.bfloat16)
+        idx = torch.randint(0, 6, (Mc,), device=dev, generator=gen)
+        st = fc.Stash(x32, sa_c, sb_c, None, torch.empty((Mc, H), device=dev, dtype=torch.bfloat16))
+        t_out = time_steps(lambda: fc.gate_rms_fused(st, resid, ada[:, 2 * H:3 * H], wn, ada[:, :H], ada[:, H:2 * H],
+                                                     idx, 1e-6), steps, warm) / steps
+        out_bytes = Mc * H * (4.0 + 2 + 2 + 2)                       # product, residual in; residual_out, h out
+        t_fc2 = time_steps(lambda: fc.gate_fused(st, resid, ada[:, 5 * H:], idx), steps, warm) / steps
+        fc2_bytes = Mc * H * (4.0 + 2 + 2)                           # product, x in; out
+        res["out_gate_rms_31248x3072"] = {"ms": round(t_out, 4), "GB/s": round(out_bytes / (t_out * 1e-3) / 1e9, 1),
+                                          "frac_hbm": round(out_bytes / (t_out * 1e-3) / 1e9 / PEAK_GBS, 4)}
+        res["fc2_indexed_gate_31248x3072"] = {"ms": round(t_fc2, 4),
+                                              "GB/s": round(fc2_bytes / (t_fc2 * 1e-3) / 1e9, 1),
+                                              "frac_hbm": round(fc2_bytes / (t_fc2 * 1e-3) / 1e9 / PEAK_GBS, 4)}
+        del x32, st, resid, ada
+        out["consumers_of_fp32_product"] = res
+
     # ---- CPU baseline: the oracle of the reference's torch CPU path on a row slice of the headline workload ----
     cpu = None
     if not args.no_cpu:
