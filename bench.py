@@ -129,6 +129,22 @@ def main() -> None:
     def want(name):
         return not only or name in only
 
+    if want("vendor"):
+        # The same GEMM through the vendor library (torch._scaled_mm -> hipBLASLt) on the same fp8 operands and
+        # per-token / per-channel scales, bf16 out: the practical reference point for kernel 2 on this chip.
+        try:
+            sa2, sb2 = sq.view(M, 1), sw.view(1, N)
+            t_v = time_steps(lambda: torch._scaled_mm(q, w.t(), sa2, sb2, out_dtype=torch.bfloat16), steps, warm) / steps
+            one = torch.ones((), device=dev)
+            t_vt = time_steps(lambda: torch._scaled_mm(q, w.t(), one, one, out_dtype=torch.bfloat16), steps, warm) / steps
+            out["vendor_gemm_qkv_960x576"] = {
+                "library": "torch._scaled_mm (hipBLASLt)",
+                "rowwise_scales_TFLOP/s": round(flops / (t_v * 1e-3) / 1e12, 1),
+                "tensorwise_scales_TFLOP/s": round(flops / (t_vt * 1e-3) / 1e12, 1),
+                "kernel2_TFLOP/s": round(gemm_tf, 1)}
+        except Exception as exc:  # noqa: BLE001
+            out["vendor_gemm_qkv_960x576"] = {"error": f"{type(exc).__name__}: {str(exc)[:160]}"}
+
     if want("c1"):
         c = synthetic.CONFIGS["c1_single_linear"]
         M1, K1, N1 = c["M"], c["K"], c["N"]
