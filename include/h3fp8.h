@@ -68,6 +68,17 @@ int h3fp8_quant_rows_amax(const void* x, int64_t ldx, int64_t M, int64_t K, cons
                           int64_t ldq, float* scale, void* stream);
 
 /*
+ * Kernel 1 on rows made of P segments: logical row m (P * seg wide) is x[p * stride_p + m * stride_m .. + seg] for
+ * p = 0 .. P-1 (element offsets), e.g. the reverse all-to-all's receive buffer [P, M, seg] (stride_p = M * seg,
+ * stride_m = seg) read as the out projection's [M, P * seg] input without unpacking it.  q [M, P * seg] (row stride
+ * ldq) and scale [M] as h3fp8_quant_rows.  seg and the strides multiples of 8, P * seg <= 16384, x 16-byte aligned,
+ * the source within 2 GiB.  Replaces ulysses_outq.quant_rows / _quant_rows_kernel (h3_tp2/ulysses_outq.py:73-93,
+ * :109-124) and fp8_quant_fuse.unpack_quant / _unpack_quant_kernel (h3_tp2/fp8_quant_fuse.py:372-385, :245-260).
+ */
+int h3fp8_quant_segments(const void* x, int64_t P, int64_t seg, int64_t stride_p, int64_t stride_m, int64_t M,
+                         void* q, int64_t ldq, float* scale, void* stream);
+
+/*
  * Kernel 2 -- scaled FP8 GEMM:  y[m,n] = round(sa[m] * (sb[n] * sum_k a[m,k] w[n,k]))  (fp32 accumulation, K
  * ascending per lane, no split-K), or round(fma(sa[m], sb[n]*acc, bias[n])) with a bias ([N], in out_dtype).
  * Replaces ops.cutlass_scaled_mm(a, b=w^T, scale_a, scale_b, out_dtype, bias) as routed by the reference:

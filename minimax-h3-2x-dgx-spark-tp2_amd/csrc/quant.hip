@@ -175,6 +175,55 @@ int check_quant_args(const void* x, int64_t ldx, int64_t M, int64_t K, const voi
     return H3FP8_OK;
 }
 
+// Rows made of P segments (the Ulysses receive buffer [P, M, seg] read as the out projection's [M, P * seg] input):
+// logical row m is x[p * stride_p + m * stride_m .. + seg] for p = 0 .. P-1.  Same arithmetic and layout as
+// quant_rows_kernel; 16-byte chunk c of the logical row is chunk c % cps of segment c / cps (cps = seg / 8).  The whole
+// source is one buffer descriptor of `bytes`, so chunks past the row read zeros through an out-of-range offset.
+template <int CPL>
+__global__ void __launch_bounds__(256) quant_segments_kernel(const uint16_t* __restrict__ x, uint32_t bytes,
+                                                             int64_t M, int cps, int P, int64_t stride_p,
+                                                             int64_t stride_m, uint8_t* __restrict__ q, int64_t ldq,
+                                                             float* __restrict__ scale) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (row >= M) return;
+    const int nchunk = cps * P;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, bytes);
+    uint4 v[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        const int p = c / cps;
+        const uint32_t off = c < nchunk ? (uint32_t)((p * stride_p + row * stride_m + 8 * (c - p * cps)) * 2) : 0x80000000u;
+        const v4u t = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 2);
+        v[j] = make_uint4(t.x, t.y, t.z, t.w);
+    }
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const uint32_t c = chunk_absmax(v[j]);
+        mx = mx > c ? mx : c;
+    }
+    const float amax = u2f(wave_max_u32(mx) << 16);
+    const float s = row_scale(amax);
+    const float inv = inv_scale(s);
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + row * ldq, (uint32_t)nchunk * 8u);
+    if (__builtin_amdgcn_readfirstlane(f2u(amax) & 0x7fffffffu) < 0x7f800000u) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint2 o = chunk_quant<true>(v[j], inv);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint2 o = chunk_quant<false>(v[j], inv);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
+        }
+    }
+    if (lane == 0) scale[row] = s;
+}
+
 }  // namespace
 
 namespace h3host {
@@ -194,6 +243,42 @@ int h3fp8_quant_rows(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, 
     int rc = check_quant_args(x, ldx, M, K, q, ldq, scale);
     if (rc) return rc;
     return launch_quant<false>(x, ldx, M, K, q, ldq, scale, nullptr, (hipStream_t)stream);
+}
+
+int h3fp8_quant_segments(const void* x, int64_t P, int64_t seg, int64_t stride_p, int64_t stride_m, int64_t M,
+                         void* q, int64_t ldq, float* scale, void* stream) {
+    H3_REQUIRE(P >= 1 && seg >= 0 && M >= 0 && stride_p >= 0 && stride_m >= 0, "quant_segments: negative size");
+    if (M == 0 || seg == 0) {
+        H3_REQUIRE(M == 0, "quant_segments: seg = 0 with rows");
+        return H3FP8_OK;
+    }
+    H3_REQUIRE(seg % 8 == 0 && stride_p % 8 == 0 && stride_m % 8 == 0,
+               "quant_segments: seg and both strides must be multiples of 8 elements");
+    H3_REQUIRE(P * seg <= 64 * 8 * 32, "quant_segments: P * seg = %lld exceeds 16384", (long long)(P * seg));
+    H3_REQUIRE(x && q && scale && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0 && ldq >= P * seg && ldq % 8 == 0,
+               "quant_segments: x 16-byte and q 8-byte aligned, ldq >= P * seg and a multiple of 8");
+    // bytes of the source that rows 0 .. M-1 reach: the largest element offset + seg
+    const int64_t span = (P - 1) * stride_p + (M - 1) * stride_m + seg;
+    H3_REQUIRE(span * 2 < 0x80000000ll, "quant_segments: the source spans more than 2 GiB");
+    const int64_t cpl = ((P * seg / 8) + 63) / 64;
+    dim3 grid((unsigned)((M + 3) / 4)), block(256);
+    const uint16_t* xp = (const uint16_t*)x;
+    const uint32_t bytes = (uint32_t)(span * 2);
+    const int cps = (int)(seg / 8);
+    hipStream_t st = (hipStream_t)stream;
+#define H3_S(N) hipLaunchKernelGGL((quant_segments_kernel<N>), grid, block, 0, st, xp, bytes, M, cps, (int)P, stride_p, \
+                                   stride_m, (uint8_t*)q, ldq, scale)
+    if (cpl <= 2) H3_S(2);
+    else if (cpl <= 4) H3_S(4);
+    else if (cpl <= 6) H3_S(6);
+    else if (cpl <= 8) H3_S(8);
+    else if (cpl <= 12) H3_S(12);
+    else if (cpl <= 16) H3_S(16);
+    else if (cpl <= 24) H3_S(24);
+    else H3_S(32);
+#undef H3_S
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
 }
 
 int h3fp8_quant_rows_amax(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row_amax, void* q,

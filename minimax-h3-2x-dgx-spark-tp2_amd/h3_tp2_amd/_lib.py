@@ -38,6 +38,7 @@ _SIGS = {
     "h3fp8_init": ([], I),
     "h3fp8_quant_rows": ([P, I64, I64, I64, P, I64, P, P], I),
     "h3fp8_quant_rows_amax": ([P, I64, I64, I64, P, P, I64, P, P], I),
+    "h3fp8_quant_segments": ([P, I64, I64, I64, I64, I64, P, I64, P, P], I),
     "h3fp8_gemm": ([P, I64, P, I64, P, I64, P, I64, P, P, I64, I, I64, I64, I64, P, P], I),
     "h3fp8_gemm_quant": ([P, I64, P, I64, P, I64, P, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P], I),
     "h3fp8_gemm_swiglu": ([P, I64, P, I64, P, I64, P, I64, P, P, I64, P, I64, I64, I64, P], I),

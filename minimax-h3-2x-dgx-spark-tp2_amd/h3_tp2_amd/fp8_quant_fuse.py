@@ -2,8 +2,8 @@
 quant protocol.
 
 Mirrors the reference's h3_tp2/fp8_quant_fuse.py host surface -- ``quant`` (:318-327), ``rms_quant`` (:330-346),
-``gate_rms_quant`` (:349-369), ``silu_mul_quant`` (:392-402), ``Pending`` (:432-450), ``_Ctx`` (:453-459),
-``_selfcheck`` / ``_pick_mode`` (:477-511), ``make_quant_forward`` (:553-576), ``_layer_post_hook`` (:579-588),
+``gate_rms_quant`` (:349-369), ``unpack_stock`` / ``unpack_quant`` (:372-385), ``silu_mul_quant`` (:392-402),
+``Pending`` (:432-450), ``_Ctx`` (:453-459), ``_selfcheck`` / ``_pick_mode`` (:477-511), ``make_quant_forward`` (:553-576), ``_layer_post_hook`` (:579-588),
 ``_quant_of`` (:591-603), ``block_plan`` (:614-645), ``make_block_forward`` (:648-670), ``_take_site`` (:673-680),
 ``_rows_ok`` (:691-693), ``make_rms_wrapper`` (:702-736), ``make_gate_rms_wrapper`` (:739-779), ``make_act_forward``
 (:806-828), ``parse_sites`` (:836-844), ``install`` (:925-1003) -- with the compute on kernel 1, the producer kernels
@@ -25,8 +25,9 @@ and the SwiGLU + quant kernel:
 The producer kernels sum the squares exactly (fp64, one rounding to fp32); a stock producer whose fp32 reduction
 rounds differently fails the self-check on some rows and its site stays stock.  ``own_producers=True`` (env
 ``H3_TP2_AMD_OWN_PRODUCERS=1``) also replaces the stock producers by the same kernels without the quant, so the fused
-and the stock forms agree by construction.  The Ulysses unpack of the out site is not part of this library;
-``install`` skips that site with a warning.
+and the stock forms agree by construction.  The out site (the Ulysses reverse exchange's unpack) exists only with
+sequence parallelism across GPUs; ``unpack_quant`` is its kernel (the receive buffer read in place), but ``install``
+skips the site with a warning: its hook lives in the multi-GPU exchange, which this single-GPU build does not carry.
 """
 from __future__ import annotations
 
@@ -82,6 +83,20 @@ def gate_rms_quant(residual, gate, branch, weight, shift, scale, indices, eps, s
     """``indexed_gate_rms_norm_scale_shift`` with the modulated output quantised per token: (residual_out bf16 [M, H],
     fp8 [M, H], scale [M, 1]); ``ph`` as in ``rms_quant``."""
     return ops.gate_rms_quant(residual, gate, branch, weight, shift, scale, indices, eps, ph)
+
+
+def unpack_stock(recv: torch.Tensor, heads: int) -> torch.Tensor:
+    """The Ulysses reverse exchange's unpack: receive [P, M, hl, d] -> [1, M, heads, d] contiguous (torch copy)."""
+    ws, m, hl, d = recv.shape
+    result = torch.empty((1, m, heads, d), dtype=recv.dtype, device=recv.device)
+    result[0].view(m, ws, hl, d).copy_(recv.transpose(0, 1))
+    return result
+
+
+def unpack_quant(recv: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The unpack + the per-token quant of the [M, P*hl*d] out-projection input, read straight from the receive buffer
+    [P, M, hl, d] (kernel 1 on P segments): (fp8 [M, P*hl*d], scale [M, 1])."""
+    return ops.quant_from_recv(recv)
 
 
 def silu_mul_quant(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

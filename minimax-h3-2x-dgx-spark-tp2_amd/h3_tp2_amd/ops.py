@@ -89,6 +89,35 @@ def quant_rows_amax(x: torch.Tensor, row_amax: torch.Tensor, q: torch.Tensor | N
     return q, scale
 
 
+def quant_segments(base: torch.Tensor, m: int, p: int, seg: int, stride_p: int, stride_m: int):
+    """Per-token FP8 quant of M rows whose row m is the P segments ``base[p*stride_p + m*stride_m : +seg]`` (element
+    offsets from ``base``'s data pointer, bf16): (q [M, P*seg] e4m3fn contiguous, scale [M, 1] fp32)
+    (h3_tp2/ulysses_outq.py:109-124)."""
+    _need_cuda(base)
+    if base.dtype != torch.bfloat16:
+        raise ValueError(f"quant_segments takes bf16, got {base.dtype}")
+    if not base.is_contiguous():
+        raise ValueError("quant_segments: base must be contiguous (segments are element offsets from its start)")
+    if m > 0 and (p - 1) * stride_p + (m - 1) * stride_m + seg > base.numel():
+        raise ValueError("quant_segments: the segments reach past the source tensor")
+    q = torch.empty((m, p * seg), device=base.device, dtype=E4M3)
+    s = torch.empty((m, 1), device=base.device, dtype=torch.float32)
+    _lib.call("h3fp8_quant_segments", base.data_ptr(), p, seg, stride_p, stride_m, m, q.data_ptr(), p * seg,
+              s.data_ptr(), _stream(base))
+    return q, s
+
+
+def quant_from_recv(recv: torch.Tensor):
+    """recv [P, M, hl, d] contiguous (a reverse all-to-all's receive buffer) -> the quant of the [M, P*hl*d] tensor the
+    unpack would have produced (row m = recv[0, m], recv[1, m], ...) (h3_tp2/ulysses_outq.py:138-143,
+    fp8_quant_fuse.py:372-385)."""
+    if recv.dim() != 4 or not recv.is_contiguous():
+        raise ValueError("recv must be a contiguous [P, M, hl, d] tensor")
+    p, m, hl, d = recv.shape
+    seg = hl * d
+    return quant_segments(recv, m, p, seg, m * seg, seg)
+
+
 # ---- kernel 2 -------------------------------------------------------------------------------------------------------
 
 def _gemm_args(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor, n_cols: int):
