@@ -198,3 +198,24 @@ def test_h_only_form_matches_the_fused_rows(cuda):
                                            idx.numpy(), EPS)
     assert np.array_equal(bits16(h), h_ref)
     assert np.array_equal(bits16(res), r_ref) and np.array_equal(bits16(h2), h2_ref)
+
+
+@pytest.mark.parametrize("gate,name", [(False, "c2_qkv_960x576_5s"), (True, "c3_ffn_1344x768_5s")])
+def test_full_size_producers(cuda, gate, name):
+    """The producers at the benchmark's full token counts (16740 and 31248 rows of 3072), against the oracle."""
+    from h3_tp2_amd import ops, synthetic
+    M, H = synthetic.CONFIGS[name]["M"], synthetic.CONFIGS[name]["K"]
+    x, w, sh, sc, gt, idx = mod_inputs(M, H, seed=M)
+    shd, scd, gd = _tables(cuda, sh, sc, gt)
+    if gate:
+        br = (torch.randn(M, H, generator=torch.Generator().manual_seed(5)) * 2).to(BF16)
+        res, q, s = ops.gate_rms_quant(x.to(cuda), gd, br.to(cuda), w.to(cuda), shd, scd, idx.to(cuda), EPS)
+        torch.cuda.synchronize()
+        r_ref, _, q_ref, s_ref = O.gate_rms_quant(bits16(x), bits16(gt), bits16(br), bits16(w), bits16(sh),
+                                                  bits16(sc), idx.numpy(), EPS)
+        _nan_aware_equal(bits16(res), r_ref, "residual_out")
+    else:
+        q, s = ops.rms_quant(x.to(cuda), w.to(cuda), shd, scd, idx.to(cuda), EPS)
+        torch.cuda.synchronize()
+        _, q_ref, s_ref = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
+    assert_quant_equal(q, s, q_ref, s_ref)

@@ -129,3 +129,26 @@ def test_gemm_swiglu_random_within_tolerance(cuda, M):
     A = O.e4m3_to_f32(bits8(a)).astype(np.float64)
     W = O.e4m3_to_f32(bits8(w)).astype(np.float64)
     check_close_swiglu(h, A @ W.T, sa, sb, abs_products(a, w))
+
+
+def test_ffn_full_size_swiglu_requant_is_the_oracle_of_the_accumulator(cuda):
+    """The 1344x768 5 s fused FFN at its full size (M = 31248, gate/up 3072 -> 2 x 8192): the fused gate/up GEMM +
+    SwiGLU + requant equals, bit for bit, the oracle's SwiGLU and quant applied to the kernel's own fp32 accumulator
+    (the raw-accumulator mode of the same GEMM), and the bf16 row of the SwiGLU form equals the oracle's too."""
+    from h3_tp2_amd import ops, synthetic
+    c = synthetic.CONFIGS["c3_ffn_1344x768_5s"]
+    M, K, F = c["M"], c["K"], c["F"]
+    x = synthetic.activations(M, K, seed=0, n_out=c["n_out"]).to(cuda)
+    a, sa = ops.quant_rows(x)
+    del x
+    w, sw = ops.quant_rows(synthetic.weight(2 * F, K, seed=2).to(cuda))
+    sa, sw = sa.view(-1), sw.view(-1)
+    q, s = ops.gemm_swiglu_quant(a, w, sa, sw)
+    h = ops.gemm_swiglu(a, w, sa, sw)
+    acc = ops.gemm(a, w, sa, sw, torch.float32)
+    torch.cuda.synchronize()
+    acc_np = f32(acc)
+    del acc
+    h_ref = O.scale_swiglu(acc_np, f32(sa), f32(sw))
+    assert np.array_equal(bits16(h), h_ref)
+    assert_quant_equal(q, s, *O.quant_rows(h_ref))
