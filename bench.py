@@ -121,7 +121,7 @@ def main() -> None:
 
     roofline = {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(gemm_tf / PEAK_TFLOPS, 4), "traffic": traffic,
-                "kernel": "gemm_kernel<bf16> (kernel 2)", "launch_ms": round(t_gemm, 4),
+                "kernel": "gemm_kernel<bf16> (kernel 2: full-tile rounds + half-tile tail)", "launch_ms": round(t_gemm, 4),
                 "flops_per_launch": flops}
     del x
 

@@ -72,6 +72,7 @@ struct GemmParams {
     int tiles_m, tiles_n;
     int group_m;
     int tile_offset;           // grouped launches: first block of this problem
+    int half_first;            // half-tile launches: the first tile (in the full-tile order) they cover
 };
 
 // block index -> (tile_m, tile_n): XCD-contiguous ranges, then GROUP_M-row groups (column-major inside a group).
@@ -201,27 +202,28 @@ __device__ __forceinline__ void issue_one(const StageIssue& S, const Loader& L, 
     }
 }
 
-// Weight-tile row of MFMA tile tn (0..3) of wave column wn.
-template <int EPI>
+// Weight-tile row of MFMA tile tn (0..3; 0..1 for a half tile) of wave column wn.
+template <int EPI, bool HALF = false>
 __device__ __forceinline__ int w_tile_row(int wn, int tn) {
+    if (HALF) return wn * 64 + 32 * tn;
     if (EPI == EPI_SWIGLU) return (tn < 2) ? (wn * 64 + 32 * tn) : (128 + wn * 64 + 32 * (tn - 2));
     return wn * 128 + 32 * tn;
 }
 
-template <int EPI>
+template <int EPI, bool HALF = false>
 __device__ __forceinline__ void read_frags(const uint8_t* stage, int wn, int wm, int lane, int sub, v8i af[4],
                                            v8i bf[4]) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) af[t] = read_frag(stage + w_tile_row<EPI>(wn, t) * ROWB, lane, sub);
+    for (int t = 0; t < (HALF ? 2 : 4); ++t) af[t] = read_frag(stage + w_tile_row<EPI, HALF>(wn, t) * ROWB, lane, sub);
 #pragma unroll
     for (int t = 0; t < 4; ++t) bf[t] = read_frag(stage + A_REGION + (wm * 128 + 32 * t) * ROWB, lane, sub);
 }
 
 // Fragment f of a sub-step: f = 0..3 weight tiles, 4..7 token tiles.
-template <int EPI>
+template <int EPI, bool HALF = false>
 __device__ __forceinline__ void read_one(const uint8_t* stage, int wn, int wm, int lane, int sub, int f, v8i af[4],
                                          v8i bf[4]) {
-    if (f < 4) af[f] = read_frag(stage + w_tile_row<EPI>(wn, f) * ROWB, lane, sub);
+    if (f < 4) af[f] = read_frag(stage + w_tile_row<EPI, HALF>(wn, f) * ROWB, lane, sub);
     else bf[f - 4] = read_frag(stage + A_REGION + (wm * 128 + 32 * (f - 4)) * ROWB, lane, sub);
 }
 
@@ -247,19 +249,23 @@ __device__ __forceinline__ int problem_of(const GroupedParams& gp, int id) {
     return i;
 }
 
-// Global tile id -> problem and tile coordinates.
-template <bool GROUPED>
+// Global tile id -> problem and tile coordinates.  A half-tile launch covers the full tiles half_first, ... of the
+// full-tile order, two half tiles (256 tokens x 128 channels, tn counted in 128-channel units) per full tile.
+template <bool GROUPED, bool HALF = false>
 __device__ __forceinline__ int locate(const GroupedParams& gp, int id, int& tm, int& tn) {
     const int pi = problem_of<GROUPED>(gp, id);
     const GemmParams& p = gp.g[pi];
-    tile_of(id - p.tile_offset, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    const int local = id - p.tile_offset;
+    tile_of(HALF ? p.half_first + (local >> 1) : local, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.group_m, tm,
+            tn);
+    if (HALF) tn = 2 * tn + (local & 1);
     return pi;
 }
 
 // Addressing of tile (tm, tn) of problem p for this wave.
 // lane l of an instruction covers row (l >> 3) of an 8-row group and LDS chunk (l & 7), i.e. logical chunk
 // (l & 7) ^ swz(row); swz depends on the row's bits 0..3, so even and odd groups of 8 rows differ.
-template <int EPI>
+template <int EPI, bool HALF = false>
 __device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn, int wave, int lane, Loader& L) {
     const uint32_t lrow = (uint32_t)(lane >> 3);
     const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz((int)lrow)), (uint32_t)((lane & 7) ^ swz((int)lrow + 8))};
@@ -269,6 +275,11 @@ __device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn,
         const int f0 = tn * (BN / 2);
         wrow0 = (wave < 2) ? (int64_t)f0 + 64 * wave : (int64_t)p.N + f0 + 64 * (wave - 2);
         wlimit = (wave < 2) ? (int64_t)p.N : 2 * (int64_t)p.N;
+    } else if (HALF) {
+        // a half tile's 128 weight rows are the shares of waves 0 and 1; waves 2 and 3 load nothing (their share of
+        // the stage is zero-filled and never read)
+        wlimit = p.N;
+        wrow0 = (wave < 2) ? (int64_t)tn * (BN / 2) + 64 * wave : wlimit;
     } else {
         wrow0 = (int64_t)tn * BN + 64 * wave;
         wlimit = p.N;
@@ -312,7 +323,7 @@ struct Cursor {
     uint32_t dsa, dsb;  // LDS addresses of this wave's share of the tile's scale set (set c % NSCALE)
 };
 
-template <int EPI, bool GROUPED>
+template <int EPI, bool GROUPED, bool HALF = false>
 __device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, int c, uint32_t lds0, int wave,
                                            int lane) {
     const int id = (int)blockIdx.x + c * (int)gridDim.x;
@@ -330,10 +341,10 @@ __device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, i
         return;
     }
     int tm, tn;
-    const int pi = locate<GROUPED>(gp, id, tm, tn);
+    const int pi = locate<GROUPED, HALF>(gp, id, tm, tn);
     const GemmParams& p = gp.g[pi];
     I.nk = (p.K + BK - 1) / BK;
-    make_loader<EPI>(p, tm, tn, wave, lane, I.L);
+    make_loader<EPI, HALF>(p, tm, tn, wave, lane, I.L);
 }
 
 // The load instructions of the cursor's k-step for this wave (wofs = the wave's 64-row share within a region).
@@ -369,9 +380,9 @@ __device__ __forceinline__ void issue_scales(uint32_t lds0, const Cursor& I) {
     dma4(I.L.rsb, real ? I.dsb : lds0 + JUNK_OFF + 256, real ? I.L.sb_off : OOB);
 }
 
-template <int EPI, bool GROUPED>
+template <int EPI, bool GROUPED, bool HALF = false>
 __device__ __forceinline__ void cursor_next(Cursor& I, const GroupedParams& gp, uint32_t lds0, int wave, int lane) {
-    if (++I.ks == I.nk) cursor_set<EPI, GROUPED>(I, gp, I.c + 1, lds0, wave, lane);
+    if (++I.ks == I.nk) cursor_set<EPI, GROUPED, HALF>(I, gp, I.c + 1, lds0, wave, lane);
 }
 
 // One k-step g (stage g & 1 holds it, its sub-step-0 fragments are in fa0/fb0, the loads of k-step g+1 are in flight;
@@ -431,6 +442,54 @@ __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const 
     }
 }
 
+// The k-step of a half tile (256 tokens x 128 channels; each wave 128 tokens x 64 channels = 2 x 4 MFMA tiles): the
+// same stage, loads and barriers as kstep, over 16 MFMAs -- u < 8 sub-step 0, u >= 8 sub-step 1:
+//   u < 6        the 6 sub-step-1 fragment reads (2 weight, 4 token tiles);
+//   u == 6       lgkmcnt(0) + barrier 1: the stage is free;
+//   6 < u < 14   the 16 load instructions of k-step g+2 and the two scale loads, three per MFMA;
+//   u == 14      vmcnt + barrier 2: k-step g+1 has landed;
+//   u >= 14      the 6 sub-step-0 fragment reads of k-step g+1.
+constexpr int HALF_REL = 6;
+constexpr int HALF_PUB = 14;
+constexpr int HALF_READ[6] = {0, 1, 4, 5, 6, 7};
+constexpr int HALF_NEXT_READ[6] = {0, 4, 5, 6, 7, 1};
+
+template <int EPI, bool READ_NEXT>
+__device__ __forceinline__ void kstep_half(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, uint32_t wofs, int wn,
+                                           int wm, int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4],
+                                           v8i fb1[4]) {
+    uint8_t* cur = lds + (g & 1) * STAGE_BYTES;
+    uint8_t* nxt = lds + ((g + 1) & 1) * STAGE_BYTES;
+    const StageIssue S = stage_issue<EPI>(lds0 + (uint32_t)(g & 1) * STAGE_BYTES, I, wofs);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        if (u < 8) mfma_one(acc, fa0, fb0, u);
+        else mfma_one(acc, fa1, fb1, u - 8);
+        if (u < 6) read_one<EPI, true>(cur, wn, wm, lane, 1, HALF_READ[u], fa1, fb1);
+        if (u == HALF_REL) {
+            wait_lgkm0();
+            barrier_nofence();
+        }
+        if (u > HALF_REL && u < HALF_PUB) {
+#pragma unroll
+            for (int k = 3 * (u - HALF_REL - 1); k < 3 * (u - HALF_REL); ++k) {
+                if (k < 16) issue_one<EPI>(S, I.L, k);
+                else if (k == 16) issue_scales(lds0, I);
+            }
+        }
+        if (u == HALF_PUB) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(18));  // k-step g+1 (and older) has landed
+            barrier_nofence();
+        }
+        if (READ_NEXT && u >= HALF_PUB) {
+#pragma unroll
+            for (int f = 3 * (u - HALF_PUB); f < 3 * (u - HALF_PUB) + 3; ++f)
+                read_one<EPI, true>(nxt, wn, wm, lane, 0, HALF_NEXT_READ[f], fa0, fb0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // max(m, |lo half|, |hi half|) of a packed bf16 pair, as fp32 bit patterns (the row maximum of the fused quant).
 __device__ __forceinline__ uint32_t max_abs_bf16x2(uint32_t m, uint32_t p) {
     const uint32_t lo = (p << 16) & 0x7fff0000u, hi = p & 0x7fff0000u;
@@ -450,9 +509,12 @@ __device__ __forceinline__ float zero_to_pos(float x) {
 // 8q + 4(l >> 5) + r of the MFMA tile and token l & 31.  The scaled, rounded outputs go through the wave's staging
 // area, 32 tokens x 64 channels at a time, so that global stores are 16-byte pieces of 128-byte row segments.
 // Scales come from the tile's scale set in LDS (loaded with the tile's first k-step).
-template <int OUT_DT, bool HAS_BIAS, int EPI>
+template <int OUT_DT, bool HAS_BIAS, int EPI, bool HALF = false>
 __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, uint8_t* lds, int set, int wave, int wn,
                                          int wm, int lane, v16f acc[4][4]) {
+    constexpr int NI = HALF ? 2 : 4;                    // MFMA tiles along the channels per wave
+    const int wcol = HALF ? tn * (BN / 2) + wn * 64 : tn * BN + wn * 128;   // the wave's first output channel
+    const int wsb = HALF ? wn * 64 : wn * 128;          // ... and its first entry in the tile's sb set
     const int hi = lane >> 5;
     const int mj = lane & 31;
     const int mrow0 = tm * BM + wm * 128;               // first token row of the wave
@@ -462,12 +524,12 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
         // probe mode: the raw fp32 accumulators, scales / bias / rounding not applied (16-byte stores per lane)
         float* yf = reinterpret_cast<float*>(p.y);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int n = tn * BN + wn * 128 + 32 * i + 8 * q + 4 * hi;
+                    const int n = wcol + 32 * i + 8 * q + 4 * hi;
                     const int m = mrow0 + 32 * j + mj;
                     if (n < p.N && m < p.M) {
                         const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
@@ -581,23 +643,23 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
             flush(mrow0 + 32 * j, col0, F);
         }
     } else {
-        const int col0 = tn * BN + wn * 128;
+        const int col0 = wcol;
         // every scale the wave needs, read once up front (one LDS round trip instead of one per group of four)
         float sa_j[4];
         v4f sb_v[4][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) sa_j[j] = sa_l[wm * 128 + 32 * j + mj];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sb_v[i][q] = *reinterpret_cast<const v4f*>(sb_l + wn * 128 + 32 * i + 8 * q + 4 * hi);
+            for (int q = 0; q < 4; ++q) sb_v[i][q] = *reinterpret_cast<const v4f*>(sb_l + wsb + 32 * i + 8 * q + 4 * hi);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = mrow0 + 32 * j + mj;
             const float sam = sa_j[j];
             uint32_t rmax = 0;
 #pragma unroll
-            for (int ip = 0; ip < 2; ++ip) {
+            for (int ip = 0; ip < NI / 2; ++ip) {
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii) {
                     const int i = 2 * ip + ii;
@@ -641,7 +703,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
 // Persistent kernel: workgroup b computes tiles b, b + G, b + 2G, ... (G = gridDim.x <= the CU count, one workgroup per
 // CU).  The load cursor runs two k-steps ahead of the MFMAs across tile boundaries, so the first two stages of the
 // next tile (and its scales) load while the current tile's last k-steps and epilogue run.
-template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED>
+template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED, bool HALF = false>
 __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_TOTAL];
 
@@ -654,7 +716,7 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     Cursor I;
     const uint32_t lds0 = lds_addr(lds);
     const uint32_t wofs = (uint32_t)wave * 64u * ROWB;  // the wave's 64-row share of a stage region
-    cursor_set<EPI, GROUPED>(I, gp, 0, lds0, wave, lane);
+    cursor_set<EPI, GROUPED, HALF>(I, gp, 0, lds0, wave, lane);
     if (!I.valid) return;
 
     // prologue: k-steps 0 and 1 (and the scales of their tiles) in flight, the sub-step-0 fragments of k-step 0 in
@@ -662,44 +724,46 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     v8i fa0[4], fb0[4], fa1[4], fb1[4];
     issue_stage<EPI>(lds0, I, wofs);
     issue_scales(lds0, I);
-    cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
+    cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
     issue_stage<EPI>(lds0 + STAGE_BYTES, I, wofs);
     issue_scales(lds0, I);
-    if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
+    if (I.valid) cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(18));
     barrier_nofence();
-    read_frags<EPI>(lds, wn, wm, lane, 0, fa0, fb0);
+    read_frags<EPI, HALF>(lds, wn, wm, lane, 0, fa0, fb0);
 
     int g = 0;
     for (int c = 0;; ++c) {
         const int id = (int)blockIdx.x + c * G;
         int tm, tn;
-        const int pi = locate<GROUPED>(gp, id, tm, tn);
+        const int pi = locate<GROUPED, HALF>(gp, id, tm, tn);
         const GemmParams& p = gp.g[pi];
         const int nk = (p.K + BK - 1) / BK;
 
-        v16f acc[4][4];
+        v16f acc[4][4];                                 // a half tile uses acc[0..1][*]
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < (HALF ? 2 : 4); ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
         for (int ks = 0; ks < nk - 1; ++ks, ++g) {
-            kstep<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-            if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
+            if (HALF) kstep_half<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+            else kstep<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+            if (I.valid) cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
         }
         // the tile's last k-step publishes the next k-step's stage but leaves its fragment registers free for the
         // epilogue; they are read after it
-        kstep<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-        if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
+        if (HALF) kstep_half<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        else kstep<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        if (I.valid) cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
         ++g;
-        epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
+        epilogue<OUT_DT, HAS_BIAS, EPI, HALF>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
         // the next tile's fragment reads stay after the epilogue: hoisted into it they would hold 64 VGPRs across it
         __builtin_amdgcn_sched_barrier(0);
         if (id + G >= gp.total_tiles) break;
-        read_frags<EPI>(lds + (g & 1) * STAGE_BYTES, wn, wm, lane, 0, fa0, fb0);
+        read_frags<EPI, HALF>(lds + (g & 1) * STAGE_BYTES, wn, wm, lane, 0, fa0, fb0);
     }
     wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
 }
@@ -719,21 +783,47 @@ int zero_rows(float* p, int64_t n, hipStream_t st) {
 // Workgroups of a persistent launch over `tiles` tiles: one per CU, at most one per tile.
 int grid_for(int tiles) { return std::max(1, std::min(tiles, h3host::cu_count())); }
 
-template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED>
+template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED, bool HALF = false>
 int launch_one(const GroupedParams& gp, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI, GROUPED>), dim3(grid_for(gp.total_tiles)), dim3(256), 0, st,
-                       gp);
+    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI, GROUPED, HALF>), dim3(grid_for(gp.total_tiles)), dim3(256), 0,
+                       st, gp);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
 
-template <int EPI>
+template <int EPI, bool HALF = false>
 int dispatch(const GroupedParams& gp, int out_dt, bool has_bias, hipStream_t st) {
     if (out_dt == H3FP8_DT_BF16) {
-        return has_bias ? launch_one<0, true, EPI, false>(gp, st) : launch_one<0, false, EPI, false>(gp, st);
+        return has_bias ? launch_one<0, true, EPI, false, HALF>(gp, st) : launch_one<0, false, EPI, false, HALF>(gp, st);
     }
-    if (out_dt == H3FP8_DT_F32) return launch_one<H3FP8_DT_F32, false, EPI_PLAIN, false>(gp, st);
-    return has_bias ? launch_one<1, true, EPI, false>(gp, st) : launch_one<1, false, EPI, false>(gp, st);
+    if (out_dt == H3FP8_DT_F32) return launch_one<H3FP8_DT_F32, false, EPI_PLAIN, false, HALF>(gp, st);
+    return has_bias ? launch_one<1, true, EPI, false, HALF>(gp, st) : launch_one<1, false, EPI, false, HALF>(gp, st);
+}
+
+// The last, partial round of a launch with full tiles leaves most CUs idle.  When its tiles fit one round as half
+// tiles (256 tokens x 128 channels, the same MFMAs per output element, so the same bits), the full-tile launch stops
+// at the last whole round and a half-tile launch covers the rest: a problem of T full tiles on G CUs runs
+// floor(T / G) full rounds and, if T mod G <= G / 2, the remainder as 2 (T mod G) half tiles.  Kernel 3 (SwiGLU pairs
+// gate and up rows inside a tile) always runs full tiles.
+int launch_split(GroupedParams gp, int epi, int out_dt, bool has_bias, hipStream_t st) {
+    const int T = gp.g[0].tiles_m * gp.g[0].tiles_n;
+    const int G = h3host::cu_count();
+    const int full = (epi == EPI_SWIGLU) ? T : (T / G) * G;
+    const int rest = T - full;
+    const bool half = rest > 0 && 2 * rest <= G;
+    const int full_tiles = half ? full : T;
+    int rc = H3FP8_OK;
+    if (full_tiles > 0) {
+        gp.total_tiles = full_tiles;
+        if (epi == EPI_PLAIN) rc = dispatch<EPI_PLAIN>(gp, out_dt, has_bias, st);
+        else if (epi == EPI_AMAX) rc = dispatch<EPI_AMAX>(gp, out_dt, has_bias, st);
+        else rc = dispatch<EPI_SWIGLU>(gp, H3FP8_DT_BF16, has_bias, st);
+        if (rc || !half) return rc;
+    }
+    gp.g[0].half_first = full_tiles;
+    gp.total_tiles = 2 * rest;
+    if (epi == EPI_PLAIN) return dispatch<EPI_PLAIN, true>(gp, out_dt, has_bias, st);
+    return dispatch<EPI_AMAX, true>(gp, out_dt, has_bias, st);
 }
 
 constexpr int64_t kMaxBufferBytes = 0x7fff0000LL;   // buffer offsets are 32-bit; keep clear of the OOB marker
@@ -800,11 +890,7 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
                               reinterpret_cast<uint8_t*>(y) + r0 * ldy * out_elem, ldy, Mi, N, K, w_rows,
                               row_amax ? row_amax + r0 : nullptr, silu, epi == EPI_SWIGLU);
         gp.n = 1;
-        gp.total_tiles = gp.g[0].tiles_m * gp.g[0].tiles_n;
-        int rc;
-        if (epi == EPI_PLAIN) rc = dispatch<EPI_PLAIN>(gp, out_dt, bias != nullptr, st);
-        else if (epi == EPI_AMAX) rc = dispatch<EPI_AMAX>(gp, out_dt, bias != nullptr, st);
-        else rc = dispatch<EPI_SWIGLU>(gp, H3FP8_DT_BF16, bias != nullptr, st);
+        const int rc = launch_split(gp, epi, out_dt, bias != nullptr, st);
         if (rc) return rc;
     }
     return H3FP8_OK;

@@ -164,3 +164,20 @@ def test_accumulator_error_model(cuda, kind, M, N, K):
     ai, wi, sai, sbi = int_operands(300, 528, 768, seed=2, device=cuda)
     acc_i = ops.gemm(ai, wi, sai, sbi, torch.float32).cpu().numpy()
     assert np.array_equal(acc_i, O.matmul_f32(bits8(ai), bits8(wi)))
+
+
+@pytest.mark.parametrize("M,N,K", [(16740, 9216, 3072), (2048, 3072, 3072), (31248, 3072, 1024)])
+def test_half_tile_tail_equals_full_tiles(cuda, M, N, K):
+    """A launch whose last round runs as half tiles (256 x 128) gives the same bits as all full tiles (the grouped
+    path never splits): the same MFMA sequence per output element.  Also the fused row maxima + quant through the
+    split launch against the oracle's quant of its own output."""
+    from h3_tp2_amd import ops
+    a, w, sa, sb = serving_like(M, N, K, seed=7, device=cuda)
+    y = _gemm(a, w, sa, sb)
+    (yg,) = ops.grouped_gemm([(a, w, sa, sb)])
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), yg.view(torch.int16))
+    y2, q, s = ops.gemm_quant(a, w, sa, sb)
+    torch.cuda.synchronize()
+    assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
+    assert_quant_equal(q, s, *oracle_quant(y2.cpu()))
