@@ -10,7 +10,10 @@ with a bf16 output (kernel 2).  A step is one quant + one GEMM over the whole to
 (the single linear, the fused FFN and the 15 s block chain at 1344x768, the grouped launch, the quant / SwiGLU-tail
 passes and the producers with the quant fused in, against the 8 TB/s HBM peak) are reported under ``workloads``.
 ``cpu_baseline`` times the CPU oracle of the reference's torch CPU path (per-token quant, fp32 product, scaled
-epilogue) on a row slice of the headline workload on this host's cores, scaled to the full token count.  Synthetic seeded inputs, random-init weights (no checkpoints).
+epilogue) on the headline workload's full token count on this host's cores, repeated for about 10 s (median run).
+The default 100 untimed warm-up steps let the chip's clock settle: over the first few tens of heavy calls the GEMM's
+launch time swings between about 345 and 460 us before it steadies.  Synthetic seeded inputs, random-init weights (no
+checkpoints).
 """
 from __future__ import annotations
 
@@ -31,11 +34,13 @@ PEAK_GBS = 8000.0             # MI355X HBM3E
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=100,
+                    help="untimed steps first (the chip's clock settles over the first few tens of heavy calls)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
-    ap.add_argument("--cpu-rows", type=int, default=8192, help="token rows of the CPU baseline sample")
+    ap.add_argument("--cpu-rows", type=int, default=0, help="token rows of the CPU baseline sample (0: all)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU baseline for at least this long")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 512 MiB device-to-device copy (the known-size kernel that scales PMC byte counts)")
     return ap.parse_args()
@@ -328,30 +333,31 @@ def main() -> None:
         del x32, st, resid, ada
         out["consumers_of_fp32_product"] = res
 
-    # ---- CPU baseline: the oracle of the reference's torch CPU path on a row slice of the headline workload ----
+    # ---- CPU baseline: the oracle of the reference's torch CPU path on the headline workload ----
     cpu = None
     if not args.no_cpu:
         sys.path.insert(0, ROOT)
         import numpy as np
 
         from oracle import oracle as O
-        rows = min(args.cpu_rows, M)
+        rows = min(args.cpu_rows, M) if args.cpu_rows > 0 else M
         xs = synthetic.activations(M, K, seed=0, n_out=c2["n_out"])[:rows]
         xb = xs.view(torch.int16).numpy().view(np.uint16)
         wb = synthetic.weight(N, K, seed=1).view(torch.int16).numpy().view(np.uint16)
         wq, swq = O.quant_rows(wb)
         O.linear(xb[:16], wq, swq)                                           # warm-up
-        best = None
-        for _ in range(2):
+        runs = []
+        while len(runs) < 3 or sum(runs) < args.cpu_seconds:
             t0 = time.perf_counter()
             O.linear(xb, wq, swq)
-            dt = time.perf_counter() - t0
-            best = dt if best is None else min(best, dt)
-        t_full = best * M / rows
+            runs.append(time.perf_counter() - t0)
+        med = sorted(runs)[len(runs) // 2]
+        t_full = med * M / rows
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         cpu = {"value": round(flops / t_full / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-               "sample": f"oracle per-token quant + numpy fp32 product + C epilogue on {rows} of {M} token rows "
-                         f"(min of 2 runs, {best:.2f} s), scaled linearly to {M} rows",
+               "sample": f"oracle per-token quant + numpy fp32 product + C epilogue on {rows} of {M} token rows, "
+                         f"median of {len(runs)} runs ({med:.2f} s each, {sum(runs):.1f} s in all)"
+                         + ("" if rows == M else f", scaled linearly to {M} rows"),
                "host_cpu_count": os.cpu_count()}
 
     line = {"metric": METRIC, "value": round(value, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
