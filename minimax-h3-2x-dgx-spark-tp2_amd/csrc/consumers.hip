@@ -5,16 +5,17 @@
 //
 //   x_d  = bf16(sa[t] * (sb[c] * acc[t, c]))  (or fma(sa, sb * acc, bias[c])), c = head * 128 + d -- the scale pass
 //   var  = fp32(sum_d x_d^2) / 128,  r = 1 / sqrt(var + eps)       (squares in fp32, summed in fp64, one rounding:
-//                                    lane l of the half sums dims 4l .. 4l + 3, then an xor butterfly over 16 .. 1)
+//                                    lane k of the head sums dims 32i + 4k + e in the order i, e = 0 .. 3, then an
+//                                    xor butterfly over 4, 2, 1)
 //   n_d  = bf16((x_d * r) * w_d)
 //   out_d = bf16(n_d * cos - n_(d+48) * sin)   d < 48,     cos / sin = rope[t, d], rope[t, d + 48]
 //           bf16(n_d * cos + n_(d-48) * sin)   48 <= d < 96, cos / sin = rope[t, d - 48], rope[t, d]
 //           n_d                                 d >= 96
 //
-// One 64-lane wave per (token, pair of heads), 4 per 256-thread workgroup: each half-wave holds one head, lane l of the
-// half dims 4l .. 4l + 3 (16-byte loads of the product and of sb); the rotation partner of lane l is lane l +- 12 of
-// the same half (one shuffle per packed pair).  The v columns of the product go through the plain scale pass
-// (h3fp8_scale_bias_cast) into the placeholder, where the attention reads them.
+// A unit is one token's group of 8 heads, one 64-lane wave: lanes 8j .. 8j + 7 hold head 8g + j, lane k of the eight
+// dims 32i + 4k .. 32i + 4k + 3 for i = 0 .. 3 (16 dims per lane, so the per-head work -- the butterfly, the two
+// divisions, the square root -- is shared by 16 dims), 4 waves per 256-thread workgroup, one unit each.  The v columns of the product go through the plain scale pass (h3fp8_scale_bias_cast) into
+// the placeholder, where the attention reads them.
 #include "h3fp8_common.h"
 
 namespace {
@@ -41,95 +42,140 @@ struct QkArgs {
     int64_t ldk_t, ldk_h;
 };
 
-// 32-lane half-wave sum in fp64 (xor butterfly over 16, 8, 4, 2, 1: stays inside each half of the wave).
-__device__ __forceinline__ double half_sum_f64(double v) {
+// Sum over the 8 lanes of a head in fp64 (xor butterfly over 4, 2, 1: stays inside each group of 8 lanes).
+__device__ __forceinline__ double group8_sum_f64(double v) {
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) {
+    for (int o = 4; o >= 1; o >>= 1) {
         const int lo = __shfl_xor(__double2loint(v), o, 64), hi = __shfl_xor(__double2hiint(v), o, 64);
         v += __hiloint2double(hi, lo);
     }
     return v;
 }
 
-__global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a) {
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return u2f(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return u2f(w & 0xffff0000u); }
+
+// Lane k of a head holds dims 32 i + 4 k + e (chunk i = 0 .. 3, e = 0 .. 3): one 16-byte load instruction covers a
+// head's 128 contiguous bytes of the product, so the loads coalesce.  The rotation partner of every rotated dim is lane
+// k ^ 4; which of its chunks it is depends on the side of the lane (k < 4 or k >= 4) -- the sender picks it.
+__global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64_t units) {
     const int lane = threadIdx.x & 63;
-    const int hl = lane & 31;                                    // lane within the head: dims 4 hl .. 4 hl + 3
+    const int k = lane & 7;
+    const bool up = k >= 4;
     const int heads = a.Hq + a.Hk;
-    const int64_t pairs = (heads + 1) / 2;                       // two heads per wave, one per half
+    const int groups = (heads + 7) / 8;
     const int64_t w = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (w >= a.T * pairs) return;
-    const int64_t t = w / pairs;
-    const int h = 2 * (int)(w - t * pairs) + (lane >> 5);
-    const bool live = h < heads;                                 // an odd head count leaves the last half idle
+    if (w >= units) return;
+    const int64_t t = w / groups;
+    const int h = 8 * (int)(w - t * groups) + (lane >> 3);
+    const bool live = h < heads;                                 // the last group of a head count not divisible by 8
     const bool isq = h < a.Hq;
-    const int64_t c = (int64_t)(live ? h : 0) * 128 + 4 * hl;    // product column of dim 4 hl
-    const v4f av = *reinterpret_cast<const v4f*>(a.acc + t * a.ld_acc + c);
-    const v4f sv = *reinterpret_cast<const v4f*>(a.sb + c);
-    const float sam = a.sa[t];
-    float x[4];
-    if (a.bias) {
-        const uint2 bw = *reinterpret_cast<const uint2*>(a.bias + c);
-        const uint32_t b2[2] = {bw.x, bw.y};
+    const int64_t c = (int64_t)(live ? h : 0) * 128 + 4 * k;     // product column of the lane's dim 4k (chunk 0)
+    // every load first: 4 x 16 B of the product and of sb, 4 x 8 B of bias and weight, the rope entries (bf16 operands
+    // in 8-byte pieces: they need only 8-byte alignment)
+    const float* ap = a.acc + t * a.ld_acc + c;
+    v4f av[4], sv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            x[e] = __builtin_fmaf(sam, sv[e] * av[e], u2f((e & 1) ? (b2[e >> 1] & 0xffff0000u) : (b2[e >> 1] << 16)));
+    for (int i = 0; i < 4; ++i) av[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(ap + 32 * i));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = *reinterpret_cast<const v4f*>(a.sb + c + 32 * i);
+    uint2 bw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        bw[i] = a.bias ? *reinterpret_cast<const uint2*>(a.bias + c + 32 * i) : make_uint2(0u, 0u);
+    const uint16_t* wp = (isq ? a.wq : a.wk) + 4 * k;
+    uint2 wb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wb[i] = *reinterpret_cast<const uint2*>(wp + 32 * i);
+    // rope entries of the rotated chunks 0 .. 2: cos at table index fd, sin at fd + 48
+    //   chunk 0: dims 4k + e < 48, fd = 4k;  chunk 1: dims 32 + 4k + e, fd = 32 + 4k (k < 4) or 4k - 16 (k >= 4);
+    //   chunk 2: dims 64 + 4k + e >= 48, fd = 16 + 4k
+    const int fdi[3] = {4 * k, up ? 4 * k - 16 : 32 + 4 * k, 16 + 4 * k};
+    v4u cr[3], sr[3];
+    if (a.rope_f32) {
+        const float* rr = reinterpret_cast<const float*>(a.rope) + t * a.ld_rope;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            cr[i] = *reinterpret_cast<const v4u*>(rr + fdi[i]);
+            sr[i] = *reinterpret_cast<const v4u*>(rr + fdi[i] + 48);
+        }
     } else {
+        const uint16_t* rr = reinterpret_cast<const uint16_t*>(a.rope) + t * a.ld_rope;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = sam * (sv[e] * av[e]);
+        for (int i = 0; i < 3; ++i) {
+            const uint2 cw = *reinterpret_cast<const uint2*>(rr + fdi[i]);
+            const uint2 sw = *reinterpret_cast<const uint2*>(rr + fdi[i] + 48);
+            cr[i] = v4u{cw.x, cw.y, 0u, 0u};
+            sr[i] = v4u{sw.x, sw.y, 0u, 0u};
+        }
     }
-    const uint32_t xb[2] = {cvt_bf16x2(x[0], x[1]), cvt_bf16x2(x[2], x[3])};   // the scale pass's one rounding
+    const float sam = a.sa[t];
+    // the scale pass, rounded once to bf16; x[4i + e] is dim 32i + 4k + e
+    float x[16];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = u2f((e & 1) ? (xb[e >> 1] & 0xffff0000u) : (xb[e >> 1] << 16));
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float p = sv[i][e] * av[i][e];
+            if (a.bias) {
+                const uint32_t bb = (e >> 1) ? bw[i].y : bw[i].x;
+                x[4 * i + e] = __builtin_fmaf(sam, p, (e & 1) ? hi_bf16(bb) : lo_bf16(bb));
+            } else {
+                x[4 * i + e] = sam * p;
+            }
+        }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t xb = cvt_bf16x2(x[2 * j], x[2 * j + 1]);
+        x[2 * j] = lo_bf16(xb);
+        x[2 * j + 1] = hi_bf16(xb);
+    }
     double ss = 0.0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ss += (double)(x[e] * x[e]);
-    ss = half_sum_f64(ss);
+    for (int d = 0; d < 16; ++d) ss += (double)(x[d] * x[d]);
+    ss = group8_sum_f64(ss);
     float var = (float)ss, hd = 128.0f, one = 1.0f;
     asm volatile("" : "+v"(hd), "+v"(one));                       // real divisions, as the stock kernel's
     var = var / hd;
     const float r = one / __builtin_sqrtf(var + a.eps);
-    const uint2 wb = *reinterpret_cast<const uint2*>((isq ? a.wq : a.wk) + 4 * hl);
-    const uint32_t nb[2] = {cvt_bf16x2((x[0] * r) * u2f(wb.x << 16), (x[1] * r) * u2f(wb.x & 0xffff0000u)),
-                            cvt_bf16x2((x[2] * r) * u2f(wb.y << 16), (x[3] * r) * u2f(wb.y & 0xffff0000u))};
-    // rotation partner: dims d +- 48 live 12 lanes away in the same half
-    const int partner = (lane & 32) | (hl < 12 ? hl + 12 : hl < 24 ? hl - 12 : hl);
-    const uint32_t pb[2] = {(uint32_t)__shfl((int)nb[0], partner, 64), (uint32_t)__shfl((int)nb[1], partner, 64)};
-    uint32_t ob[2] = {nb[0], nb[1]};
-    if (hl < 24) {
-        const int fd = hl < 12 ? 4 * hl : 4 * hl - 48;
-        float cs[4], sn[4];
-        if (a.rope_f32) {
-            const float* rr = reinterpret_cast<const float*>(a.rope) + t * a.ld_rope;
-            const v4f cv = *reinterpret_cast<const v4f*>(rr + fd);
-            const v4f sv2 = *reinterpret_cast<const v4f*>(rr + fd + 48);
+    uint32_t nb[8];                                              // packed pairs: nb[2i], nb[2i + 1] = chunk i
 #pragma unroll
-            for (int e = 0; e < 4; ++e) { cs[e] = cv[e]; sn[e] = sv2[e]; }
-        } else {
-            const uint16_t* rr = reinterpret_cast<const uint16_t*>(a.rope) + t * a.ld_rope;
-            const uint2 cw = *reinterpret_cast<const uint2*>(rr + fd);
-            const uint2 sw = *reinterpret_cast<const uint2*>(rr + fd + 48);
-            const uint32_t c2[2] = {cw.x, cw.y}, s2[2] = {sw.x, sw.y};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                cs[e] = u2f((e & 1) ? (c2[e >> 1] & 0xffff0000u) : (c2[e >> 1] << 16));
-                sn[e] = u2f((e & 1) ? (s2[e >> 1] & 0xffff0000u) : (s2[e >> 1] << 16));
-            }
-        }
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float n = u2f((e & 1) ? (nb[e >> 1] & 0xffff0000u) : (nb[e >> 1] << 16));
-            const float p = u2f((e & 1) ? (pb[e >> 1] & 0xffff0000u) : (pb[e >> 1] << 16));
-            const float u = n * cs[e], v = p * sn[e];
-            o[e] = hl < 12 ? u - v : u + v;
-        }
-        ob[0] = cvt_bf16x2(o[0], o[1]);
-        ob[1] = cvt_bf16x2(o[2], o[3]);
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t ww = (j & 1) ? wb[j >> 1].y : wb[j >> 1].x;
+        nb[j] = cvt_bf16x2((x[2 * j] * r) * lo_bf16(ww), (x[2 * j + 1] * r) * hi_bf16(ww));
     }
+    // the partner chunk of target chunk i: lanes k < 4 take chunk (i + 1) % 3 of lane k + 4, lanes k >= 4 chunk
+    // (i + 2) % 3 of lane k - 4, so lane k sends chunk (i + 1) % 3 if k >= 4 and (i + 2) % 3 if k < 4
+    uint32_t ob[8];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int cu = (i + 1) % 3, cl = (i + 2) % 3;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t send = up ? nb[2 * cu + q] : nb[2 * cl + q];
+            const uint32_t pb = (uint32_t)__shfl_xor((int)send, 4, 64);
+            float cs[2], sn[2];
+            if (a.rope_f32) {
+                cs[0] = u2f(cr[i][2 * q]); cs[1] = u2f(cr[i][2 * q + 1]);
+                sn[0] = u2f(sr[i][2 * q]); sn[1] = u2f(sr[i][2 * q + 1]);
+            } else {
+                cs[0] = lo_bf16(cr[i][q]); cs[1] = hi_bf16(cr[i][q]);
+                sn[0] = lo_bf16(sr[i][q]); sn[1] = hi_bf16(sr[i][q]);
+            }
+            const uint32_t n = nb[2 * i + q];
+            const float u0 = lo_bf16(n) * cs[0], v0 = lo_bf16(pb) * sn[0];
+            const float u1 = hi_bf16(n) * cs[1], v1 = hi_bf16(pb) * sn[1];
+            const bool minus = i == 0 || (i == 1 && !up);        // dims below 48
+            ob[2 * i + q] = minus ? cvt_bf16x2(u0 - v0, u1 - v1) : cvt_bf16x2(u0 + v0, u1 + v1);
+        }
+    }
+    ob[6] = nb[6];                                               // chunk 3: dims 96 + 4k + e, not rotated
+    ob[7] = nb[7];
     if (!live) return;
-    uint16_t* out = isq ? a.out_q + t * a.ldq_t + (int64_t)h * a.ldq_h
-                        : a.out_k + t * a.ldk_t + (int64_t)(h - a.Hq) * a.ldk_h;
-    *reinterpret_cast<uint2*>(out + 4 * hl) = make_uint2(ob[0], ob[1]);
+    uint16_t* out = (isq ? a.out_q + t * a.ldq_t + (int64_t)h * a.ldq_h
+                         : a.out_k + t * a.ldk_t + (int64_t)(h - a.Hq) * a.ldk_h) + 4 * k;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint2*>(out + 32 * i) = make_uint2(ob[2 * i], ob[2 * i + 1]);
 }
 
 }  // namespace
@@ -164,9 +210,9 @@ int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, 
     a.rope = rope; a.ld_rope = ld_rope; a.rope_f32 = rope_f32 ? 1 : 0; a.eps = eps;
     a.out_q = (uint16_t*)out_q; a.ldq_t = ldq_t; a.ldq_h = ldq_h;
     a.out_k = (uint16_t*)out_k; a.ldk_t = ldk_t; a.ldk_h = ldk_h;
-    const int64_t waves = T * ((Hq + Hk + 1) / 2);
-    hipLaunchKernelGGL(scale_qk_norm_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
-                       a);
+    const int64_t units = T * ((Hq + Hk + 7) / 8);
+    hipLaunchKernelGGL(scale_qk_norm_rope_kernel, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       a, units);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }

@@ -64,6 +64,7 @@ struct RmsArgs {
 };
 
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // Range-checked 16-byte chunk c of a row described by `r` (chunks past the row's end read as zero, stores there are
 // dropped): branch-free, so every load of a wave is in flight at once.
@@ -85,9 +86,14 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
+// The clamp to [-448, 448].  On a row whose maximum is finite it never changes the code: |h| <= amax, scale =
+// RNE(amax / 448) (or the floor, which only makes it larger), inv = RNE(1 / scale), so |h * inv| <= 448 (1 + 2^-24)^3
+// < 448.0001, and the conversion rounds everything below 464 (the midpoint to the next binade's 480, which e4m3fn
+// lacks) to 448 -- so the finite path converts without it.  Rows with inf or NaN keep the compare / select form
+// (NaN propagates, +-inf saturates).
 template <bool FINITE>
 __device__ __forceinline__ float clamp448(float y) {
-    if (FINITE) return __builtin_amdgcn_fmed3f(y, -H3_FP8_MAX, H3_FP8_MAX);
+    if (FINITE) return y;
     y = (y < -H3_FP8_MAX) ? -H3_FP8_MAX : y;
     return (y > H3_FP8_MAX) ? H3_FP8_MAX : y;
 }
@@ -124,7 +130,9 @@ __device__ __forceinline__ v4u tab16(const GlobalTables& t, int which, int c) {
 // B32 (gate form only): the branch is the scaled-GEMM epilogue of the fp32 product `acc` (the consumer of the out /
 // fc2 projection reading the accumulator instead of a bf16 output).  NORM = false stops after residual_out: that is
 // the fc2 site's indexed_gate, out = bf16(x + gate[i] * branch).
-template <bool GATE, int OUT, int CPL, bool EARLY, bool B32, bool NORM, class MakeTables>
+//
+// FULL: H == 512 CPL, every chunk of every lane lies in the row (no masking of the chunks past its end).
+template <bool GATE, int OUT, int CPL, bool EARLY, bool B32, bool NORM, bool FULL, class MakeTables>
 __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, int lane, MakeTables tables) {
     constexpr bool QUANT = (OUT & 1) != 0, WRITE_H = (OUT & 2) != 0;
     const uint32_t rb = (uint32_t)a.H * 2u;
@@ -200,7 +208,7 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
         const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.residual_out + m * a.ld_res, rb);
 #pragma unroll
         for (int j = 0; j < (GATE ? CPL : 1); ++j) {
-            const bool in = lane + 64 * j < nchunk;
+            const bool in = FULL || lane + 64 * j < nchunk;
             v4u u;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -217,11 +225,14 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
     // sum of squares: each square is exact in fp32, the fp64 sum rounds once to fp32 (chunks past the row add +0;
     // a poisoned row's NaN makes the sum NaN)
     double ss = 0.0;
+    float xf[CPL][8];                                   // the row in fp32, kept for the modulation
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float f0 = u2f(xv[j][k] << 16), f1 = u2f(xv[j][k] & 0xffff0000u);
+            xf[j][2 * k] = f0;
+            xf[j][2 * k + 1] = f1;
             ss += (double)(f0 * f0);
             ss += (double)(f1 * f1);
         }
@@ -234,12 +245,13 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
     float one = 1.0f;
     asm volatile("" : "+v"(one));
     const float r = bad ? u2f(0x7fc00000u) : one / d;  // IEEE division (torch's CPU rsqrt: 1 / sqrt)
-    // modulation, bf16 rounding, row maximum
+    // modulation, bf16 rounding, row maximum (of the packed |h| pairs, two 16-bit lanes at a time; NaN patterns order
+    // above +inf)
     v4u h[CPL];
-    uint32_t mx = 0;
+    u16x2 mx2 = {0, 0};
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const bool in = lane + 64 * j < nchunk;
+        const bool in = FULL || lane + 64 * j < nchunk;
         const v4u wv = EARLY ? wv_e[EARLY ? j : 0] : tab16(t, 0, lane + 64 * j);
         const v4u sh = EARLY ? sh_e[EARLY ? j : 0] : tab16(t, 1, lane + 64 * j);
         const v4u sc = EARLY ? sc_e[EARLY ? j : 0] : tab16(t, 2, lane + 64 * j);
@@ -248,7 +260,7 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
             float o[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const float xe = u2f(e ? (xv[j][k] & 0xffff0000u) : (xv[j][k] << 16));
+                const float xe = xf[j][2 * k + e];
                 const float we = u2f(e ? (wv[k] & 0xffff0000u) : (wv[k] << 16));
                 const float se = u2f(e ? (sc[k] & 0xffff0000u) : (sc[k] << 16));
                 const float be = u2f(e ? (sh[k] & 0xffff0000u) : (sh[k] << 16));
@@ -257,11 +269,10 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
                 o[e] = n * g + be;
             }
             h[j][k] = in ? cvt_bf16x2(o[0], o[1]) : 0u;   // chunks past the row: +0, the maximum is unchanged
-            const uint32_t lo = (h[j][k] << 16) & 0x7fff0000u, hi = h[j][k] & 0x7fff0000u;
-            mx = mx > lo ? mx : lo;
-            mx = mx > hi ? mx : hi;
+            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][k] & 0x7fff7fffu));
         }
     }
+    uint32_t mx = (uint32_t)(mx2[0] > mx2[1] ? mx2[0] : mx2[1]) << 16;   // as fp32 bits
     float s = 0.0f;
     if (QUANT) {
         mx = wave_max_u32(mx);
@@ -287,12 +298,12 @@ __device__ __forceinline__ int64_t row_index(const RmsArgs& a, int64_t m, bool& 
 }
 
 // Tables read from global memory: one wave per row, 4 rows per 256-thread workgroup.
-template <bool GATE, int OUT, int CPL, bool B32 = false, bool NORM = true>
+template <bool GATE, int OUT, int CPL, bool B32, bool NORM, bool FULL>
 __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     const int lane = threadIdx.x & 63;
     const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (m >= a.M) return;
-    rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 8 && !B32), B32, NORM>(a, m, lane, [&](bool& bad) {
+    rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 8 && !B32), B32, NORM, FULL>(a, m, lane, [&](bool& bad) {
         const int64_t i = row_index(a, m, bad);
         const uint32_t rb = (uint32_t)a.H * 2u;
         GlobalTables t;
@@ -306,8 +317,11 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
 
 template <bool GATE, int OUT, int CPL, bool B32, bool NORM>
 int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, NORM>), dim3((unsigned)((a.M + 3) / 4)), dim3(256), 0,
-                       st, a);
+    const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
+    if (a.H == 512 * CPL)
+        hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, NORM, true>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, NORM, false>), grid, block, 0, st, a);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }

@@ -273,6 +273,58 @@ __global__ void __launch_bounds__(256) scale_bias_cast_kernel(const float* __res
     *reinterpret_cast<uint2*>(y + m * ldy + n) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
 }
 
+// The scale pass over row segments, for contiguous (16-byte aligned) sb and an 8-byte aligned bias: block (m, s) covers
+// the U * 256 column groups of segment s of row m, thread i the groups i + 256 u (coalesced per u).  Every load is a
+// range-checked buffer load (groups past the row read zero and their stores are dropped), so all U groups' loads are
+// in flight before the first use; no per-thread division.
+template <int OUT_DT, int U>
+__global__ void __launch_bounds__(256) scale_bias_cast_seg_kernel(const float* __restrict__ x, int64_t ldx, int64_t N,
+                                                                  EpiArgs e, uint16_t* __restrict__ y, int64_t ldy) {
+    const int64_t m = blockIdx.x;
+    const uint32_t g0 = blockIdx.y * (256u * U) + threadIdx.x;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + m * ldx, (uint32_t)N * 4u);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(e.sb, (uint32_t)N * 4u);
+    const bool hb = e.bias != nullptr;
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(hb ? (const void*)e.bias : (const void*)e.sb, hb ? (uint32_t)N * 2u : 0u);
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(y + m * ldy, (uint32_t)N * 2u);
+    v4u xv[U], sv[U];
+    v2u bv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t g = g0 + 256u * u;
+        xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, g * 16u, 0, 2);     // streamed once: non-temporal
+        sv[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, g * 16u, 0, 0);
+        bv[u] = __builtin_amdgcn_raw_buffer_load_b64(br, g * 8u, 0, 0);        // zeros without a bias
+    }
+    const float sam = e.sa[m * e.sa_stride];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        uint32_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t bw = bv[u][r >> 1];
+            const uint32_t bh = (r & 1) ? (bw >> 16) : (bw & 0xffffu);
+            const float b = OUT_DT ? fp16_to_f32(bh) : bf16_to_f32(bh);
+            const float val = epi(u2f(xv[u][r]), sam, u2f(sv[u][r]), hb, b);
+            o[r] = OUT_DT ? fp16_rne(val) : bf16_rne(val);
+        }
+        const v2u ov = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        __builtin_amdgcn_raw_buffer_store_b64(ov, yr, (g0 + 256u * u) * 8u, 0, 0);
+    }
+}
+
+template <int OUT_DT>
+void launch_scale_bias_cast_seg(const float* x, int64_t ldx, int64_t M, int64_t N, const EpiArgs& e, uint16_t* y,
+                                int64_t ldy, hipStream_t st) {
+    const int64_t groups = N >> 2;
+    const int u = (int)std::min<int64_t>(4, (groups + 255) / 256);
+    dim3 grid((unsigned)M, (unsigned)((groups + 256 * u - 1) / (256 * u))), block(256);
+    if (u <= 1) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 1>), grid, block, 0, st, x, ldx, N, e, y, ldy);
+    else if (u == 2) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 2>), grid, block, 0, st, x, ldx, N, e, y, ldy);
+    else if (u == 3) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 3>), grid, block, 0, st, x, ldx, N, e, y, ldy);
+    else hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 4>), grid, block, 0, st, x, ldx, N, e, y, ldy);
+}
+
 // The persistent LDS-table form of the bf16-source pass, when its 16-byte loads and 8-byte stores are aligned and a row
 // fits in registers (F <= 8192); returns false to take the one-workgroup-per-row kernel instead.
 bool launch_silu_mul_quant_lds(const void* x, int64_t ldx, int64_t M, int64_t F, const uint16_t* silu, void* q,
@@ -345,6 +397,15 @@ int h3fp8_scale_bias_cast(const float* x32, int64_t ldx, const float* sa, int64_
     H3_REQUIRE(sa && sb && y && ldy >= N && ldy % 4 == 0 && ((uintptr_t)y & 7) == 0,
                "h3fp8_scale_bias_cast: bad scales or output");
     EpiArgs e{sa, sa_stride, sb, sb_stride, (const uint16_t*)bias};
+    if (sb_stride == 1 && ((uintptr_t)sb & 15) == 0 && ((uintptr_t)bias & 7) == 0 && N < ((int64_t)1 << 30) &&
+        M < ((int64_t)1 << 31)) {
+        if (out_dtype == H3FP8_DT_BF16)
+            launch_scale_bias_cast_seg<0>(x32, ldx, M, N, e, (uint16_t*)y, ldy, (hipStream_t)stream);
+        else
+            launch_scale_bias_cast_seg<1>(x32, ldx, M, N, e, (uint16_t*)y, ldy, (hipStream_t)stream);
+        H3_CHECK_HIP(hipGetLastError());
+        return H3FP8_OK;
+    }
     const int64_t total = M * (N >> 2);
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     if (out_dtype == H3FP8_DT_BF16)

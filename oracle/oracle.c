@@ -352,18 +352,20 @@ void oracle_gate_rms_quant(const uint16_t* residual, int64_t ldr, const uint16_t
  *   pair(d) = d + 48 (d < 48), d - 48 (48 <= d < 96), d;  freq(d) = d (d < 48), d - 48 (48 <= d < 96), 0
  *   c = table[freq(d)], s = table[freq(d) + 48]
  *   out_d = bf16(n_d * c - n_pair * s) (d < 48), bf16(n_d * c + n_pair * s) (48 <= d < 96), n_d (d >= 96)
- * The sum of squares is rounded once to fp32 from an fp64 sum in the HIP kernel's order: lane l of 32 adds the squares
- * of dims 4l .. 4l + 3, then an xor butterfly over the 32 lane sums (distances 16, ..., 1). */
+ * The sum of squares is rounded once to fp32 from an fp64 sum in the HIP kernel's order: lane l of 8 adds the squares
+ * of dims 32i + 4l + e in the order i = 0 .. 3, e = 0 .. 3, then an xor butterfly over the 8 lane sums (distances 4,
+ * 2, 1). */
 static double head_sumsq(const float* x) {
-    double p[32];
-    for (int l = 0; l < 32; ++l) {
+    double p[8];
+    for (int l = 0; l < 8; ++l) {
         double s = 0.0;
-        for (int e = 0; e < 4; ++e) s += (double)(x[4 * l + e] * x[4 * l + e]);
+        for (int i = 0; i < 4; ++i)
+            for (int e = 0; e < 4; ++e) s += (double)(x[32 * i + 4 * l + e] * x[32 * i + 4 * l + e]);
         p[l] = s;
     }
-    for (int d = 16; d >= 1; d >>= 1) {
-        double t[32];
-        for (int l = 0; l < 32; ++l) t[l] = p[l] + p[l ^ d];
+    for (int d = 4; d >= 1; d >>= 1) {
+        double t[8];
+        for (int l = 0; l < 8; ++l) t[l] = p[l] + p[l ^ d];
         memcpy(p, t, sizeof(p));
     }
     return p[0];

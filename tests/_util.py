@@ -209,3 +209,33 @@ def rope_table(T: int, dtype, seed: int = 3):
     g = torch.Generator().manual_seed(seed)
     pos = torch.rand(T, 1, generator=g) * 500 * torch.exp(-torch.arange(48) / 8.0)[None, :]
     return torch.cat((torch.cos(pos), torch.sin(pos)), dim=-1).to(dtype)
+
+
+# A 128-dim head whose fp32 sum of squares depends on the reduction order: its fp64 sum sits on an fp32 rounding tie
+# (large squares that are multiples of the fp32 ulp plus 2^17 squared, half an ulp), and the small squares tip it only
+# when they are summed among themselves before they meet the large ones.  With weight ORDER_W at dim ORDER_DIM the
+# normalised bf16 output of that dim differs between the kernel's lane order (KERNEL_LANES: lane k adds dims
+# 32i + 4k + e in the order i, e = 0 .. 3, then an xor butterfly over 4, 2, 1) and a 32 x 4 one (CONTIG32_LANES), so a
+# kernel that reduces in another order fails it.
+ORDER_HEAD = {15: 4.0, 31: 131072.0, 41: -4.0, 47: 2.0, 48: 62128128.0, 53: -4.0, 64: 50593792.0, 66: 3.0, 76: -4.0,
+              79: 557842432.0, 106: 2.0, 118: -4.0, 126: 4.0}
+ORDER_DIM, ORDER_W = 31, 1.40625
+KERNEL_LANES = [[32 * i + 4 * k + e for i in range(4) for e in range(4)] for k in range(8)]
+CONTIG32_LANES = [[4 * k + e for e in range(4)] for k in range(32)]
+
+
+def lane_order_sumsq(x, lanes) -> float:
+    """fp64 sum of the fp32 squares of a 128-dim head: lane l adds the squares of the dims lanes[l] in that order, then
+    an xor butterfly over the lane sums (largest distance first); rounded to fp32."""
+    import numpy as np
+    p = []
+    for dims in lanes:
+        s = 0.0
+        for d in dims:
+            s += float(np.float32(x[d]) * np.float32(x[d]))
+        p.append(s)
+    d = len(p) // 2
+    while d >= 1:
+        p = [p[l] + p[l ^ d] for l in range(len(p))]
+        d //= 2
+    return float(np.float32(p[0]))

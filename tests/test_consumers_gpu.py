@@ -70,6 +70,34 @@ def test_qk_norm_rope_matches_oracle(cuda, T, H, Hk, bias, rope_dtype):
     assert v.data_ptr() == st.ph.data_ptr() + (H + Hk) * D * 2
 
 
+def test_qk_norm_rope_sum_order(cuda):
+    """A head whose fp32 sum of squares depends on the reduction order (tests/_util.py): as a q and a k head, with
+    and without a rotation, the kernel's output equals the oracle's, whose order the CPU suite pins."""
+    from _util import ORDER_DIM, ORDER_HEAD, ORDER_W
+    from h3_tp2_amd import fp8_consumers as fc
+    D, T = 128, 2
+    x32 = torch.zeros(T, 3 * D)
+    for d, v in ORDER_HEAD.items():
+        x32[:, d] = v
+        x32[:, D + d] = v
+    x32[:, 2 * D:] = 1.0
+    sa, sb = torch.ones(T), torch.ones(3 * D)
+    w = torch.ones(D)
+    w[ORDER_DIM] = ORDER_W
+    w = w.to(BF16)
+    rope = rope_table(T, torch.float32)
+    rope[0, :48], rope[0, 48:] = 1.0, 0.0                       # token 0: no rotation
+    x32d, sad, sbd, wd, roped = _dev(x32, sa, sb, w, rope, cuda=cuda)
+    st = fc.Stash(x32d, sad, sbd, None, torch.empty((T, 3 * D), dtype=BF16, device=cuda))
+    oq, ok, _ = fc.qk_norm_rope_fused(st, 1, 1, D, wd, wd, roped, EPS)
+    torch.cuda.synchronize()
+    p = _epi(x32, sa, sb, None)
+    assert np.array_equal(p[:, :2 * D], O.bf16_bits_from_f32(x32[:, :2 * D].numpy()))
+    ref = O.qk_norm_rope(p[:, :D].reshape(T, 1, D), bits16(w), rope.numpy(), EPS)
+    _nan_aware_equal(bits16(oq), ref, "q")
+    _nan_aware_equal(bits16(ok), ref, "k")
+
+
 @pytest.mark.parametrize("T,hidden", [(1, 128), (37, 200), (64, 256), (1000, 3072), (300, 5376)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gate_rms_matches_oracle(cuda, T, hidden, bias):

@@ -517,3 +517,25 @@ def test_qk_norm_rope_matches_the_torch_standin(rope_dtype):
     big = np.abs(O.bf16_to_f32(out)).max(axis=-1, keepdims=True) * 3
     tol = np.maximum(np.abs(a), np.abs(b)) * 2.0 ** -7 + big * 2.0 ** -7
     assert (np.abs(a - b) <= tol)[~same].all()
+
+
+def test_qk_head_sum_order_is_pinned():
+    """The order-sensitive head: the oracle's normalised output equals the one computed from the kernel's lane order's
+    sum and differs from a 32 x 4 order's (so the GPU comparison against the oracle pins the kernel's order)."""
+    from _util import CONTIG32_LANES, KERNEL_LANES, ORDER_DIM, ORDER_HEAD, ORDER_W, lane_order_sumsq
+    x = np.zeros(128, np.float32)
+    for d, v in ORDER_HEAD.items():
+        x[d] = v
+    s8, s32 = lane_order_sumsq(x, KERNEL_LANES), lane_order_sumsq(x, CONTIG32_LANES)
+    assert s8 != s32
+    w = np.ones(128, np.float32)
+    w[ORDER_DIM] = ORDER_W
+    ident = np.concatenate([np.ones((1, 48)), np.zeros((1, 48))], axis=1).astype(np.float32)
+    out = O.qk_norm_rope(O.bf16_bits_from_f32(x).reshape(1, 1, 128), O.bf16_bits_from_f32(w), ident, 1e-6)
+
+    def norm(var):
+        v = np.float32(np.float32(var) / np.float32(128.0))
+        r = np.float32(1.0) / np.sqrt(np.float32(v + np.float32(1e-6)))
+        return O.bf16_bits_from_f32(np.array([np.float32(x[ORDER_DIM] * r) * np.float32(ORDER_W)], np.float32))[0]
+    assert out[0, 0, ORDER_DIM] == norm(s8)
+    assert norm(s8) != norm(s32)
