@@ -123,16 +123,16 @@ __device__ __forceinline__ v4u tab16(const GlobalTables& t, int which, int c) {
 }
 // One row m processed by one wave.  OUT: bit 0 = the e4m3 row and its scale, bit 1 = the bf16 modulated row (h only:
 // the stock producer itself).  EARLY: every table chunk is fetched together with the row (their latency overlaps the
-// row's instead of following the reduction); above 8 chunks per lane the registers do not allow it.
+// row's instead of following the reduction); above 8 chunks per lane (6 for the fp32-branch form) the registers do
+// not allow it.
 // `tables(bad)` returns the row's table source and sets `bad` (index out of range); it is called after the row's own
 // loads are issued, so the index load and the table loads that depend on it overlap the row's latency.
 //
-// B32 (gate form only): the branch is the scaled-GEMM epilogue of the fp32 product `acc` (the consumer of the out /
-// fc2 projection reading the accumulator instead of a bf16 output).  NORM = false stops after residual_out: that is
-// the fc2 site's indexed_gate, out = bf16(x + gate[i] * branch).
+// B32 (gate form only): the branch is the scaled-GEMM epilogue of the fp32 product `acc` (the consumer of the out
+// projection reading the accumulator instead of a bf16 output).
 //
 // FULL: H == 512 CPL, every chunk of every lane lies in the row (no masking of the chunks past its end).
-template <bool GATE, int OUT, int CPL, bool EARLY, bool B32, bool NORM, bool FULL, class MakeTables>
+template <bool GATE, int OUT, int CPL, bool EARLY, bool B32, bool FULL, class MakeTables>
 __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, int lane, MakeTables tables) {
     constexpr bool QUANT = (OUT & 1) != 0, WRITE_H = (OUT & 2) != 0;
     const uint32_t rb = (uint32_t)a.H * 2u;
@@ -221,7 +221,6 @@ __device__ __forceinline__ void rms_mod_quant_row(const RmsArgs& a, int64_t m, i
             st16(u, ro, lane + 64 * j);
         }
     }
-    if (!NORM) return;
     // sum of squares: each square is exact in fp32, the fp64 sum rounds once to fp32 (chunks past the row add +0;
     // a poisoned row's NaN makes the sum NaN)
     double ss = 0.0;
@@ -298,12 +297,12 @@ __device__ __forceinline__ int64_t row_index(const RmsArgs& a, int64_t m, bool& 
 }
 
 // Tables read from global memory: one wave per row, 4 rows per 256-thread workgroup.
-template <bool GATE, int OUT, int CPL, bool B32, bool NORM, bool FULL>
+template <bool GATE, int OUT, int CPL, bool B32, bool FULL>
 __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     const int lane = threadIdx.x & 63;
     const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (m >= a.M) return;
-    rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 8 && !B32), B32, NORM, FULL>(a, m, lane, [&](bool& bad) {
+    rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 6 || (CPL <= 8 && !B32)), B32, FULL>(a, m, lane, [&](bool& bad) {
         const int64_t i = row_index(a, m, bad);
         const uint32_t rb = (uint32_t)a.H * 2u;
         GlobalTables t;
@@ -315,26 +314,26 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     });
 }
 
-template <bool GATE, int OUT, int CPL, bool B32, bool NORM>
+template <bool GATE, int OUT, int CPL, bool B32>
 int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
     if (a.H == 512 * CPL)
-        hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, NORM, true>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, true>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, NORM, false>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((rms_mod_quant_kernel<GATE, OUT, CPL, B32, false>), grid, block, 0, st, a);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
 
-template <bool GATE, int OUT, bool B32 = false, bool NORM = true>
+template <bool GATE, int OUT, bool B32 = false>
 int launch_rms(const RmsArgs& a, hipStream_t st) {
     const int64_t cpl = ((a.H >> 3) + 63) / 64;
-    if (cpl <= 2) return launch_rms_cpl<GATE, OUT, 2, B32, NORM>(a, st);
-    if (cpl <= 4) return launch_rms_cpl<GATE, OUT, 4, B32, NORM>(a, st);
-    if (cpl <= 6) return launch_rms_cpl<GATE, OUT, 6, B32, NORM>(a, st);
-    if (cpl <= 8) return launch_rms_cpl<GATE, OUT, 8, B32, NORM>(a, st);
-    if (cpl <= 12) return launch_rms_cpl<GATE, OUT, 12, B32, NORM>(a, st);
-    return launch_rms_cpl<GATE, OUT, 16, B32, NORM>(a, st);
+    if (cpl <= 2) return launch_rms_cpl<GATE, OUT, 2, B32>(a, st);
+    if (cpl <= 4) return launch_rms_cpl<GATE, OUT, 4, B32>(a, st);
+    if (cpl <= 6) return launch_rms_cpl<GATE, OUT, 6, B32>(a, st);
+    if (cpl <= 8) return launch_rms_cpl<GATE, OUT, 8, B32>(a, st);
+    if (cpl <= 12) return launch_rms_cpl<GATE, OUT, 12, B32>(a, st);
+    return launch_rms_cpl<GATE, OUT, 16, B32>(a, st);
 }
 
 int check_rows(const void* p, int64_t ld, int64_t H, const char* what, const char* who) {
@@ -371,6 +370,72 @@ int check_rms(const RmsArgs& a, bool gate, bool b32, bool norm, const char* who)
     if (a.q)
         H3_REQUIRE(a.qscale && a.ldq >= a.H && a.ldq % 8 == 0 && ((uintptr_t)a.q & 7) == 0,
                    "%s: q must be 8-byte aligned with a row stride >= H and a multiple of 8, with a scale vector", who);
+    return H3FP8_OK;
+}
+
+// indexed_gate of the fc2 site reading the fp32 product: out = bf16(x + gate[i] * branch), branch = the scale pass's
+// bf16(sa * (sb * acc)) (or its fma with the bias) -- elementwise, so no row needs to stay in registers.  Block (m, s)
+// covers U * 256 groups of 4 columns of row m, thread t the groups t + 256 u (coalesced per u).  Every access is a
+// range-checked buffer load or store (groups past the row read zero and are not written); the row's own loads go out
+// before the index, the gate row's after it.  An index outside the table reads gate row 0 and writes NaN.
+template <int U>
+__global__ void __launch_bounds__(256) scale_indexed_gate_seg_kernel(RmsArgs a) {
+    const int64_t m = blockIdx.x;
+    const uint32_t g0 = blockIdx.y * (256u * U) + threadIdx.x;
+    const uint32_t H = (uint32_t)a.H;
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.acc + m * a.ld_acc, H * 4u);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sb, H * 4u);
+    const bool hb = a.bias != nullptr;
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(hb ? (const void*)a.bias : (const void*)a.sb, hb ? H * 2u : 0u);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + m * a.ldx, H * 2u);
+    v4u av[U], sv[U];
+    v2u bv[U], xv[U], gv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t g = g0 + 256u * u;
+        av[u] = __builtin_amdgcn_raw_buffer_load_b128(ar, g * 16u, 0, 2);    // streamed once: non-temporal
+        xv[u] = __builtin_amdgcn_raw_buffer_load_b64(xr, g * 8u, 0, 2);
+        sv[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, g * 16u, 0, 0);
+        bv[u] = __builtin_amdgcn_raw_buffer_load_b64(br, g * 8u, 0, 0);       // zeros without a bias
+    }
+    bool bad;
+    const int64_t i = row_index(a, m, bad);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gate + i * a.ld_gate, H * 2u);
+#pragma unroll
+    for (int u = 0; u < U; ++u) gv[u] = __builtin_amdgcn_raw_buffer_load_b64(gr, (g0 + 256u * u) * 8u, 0, 0);
+    const uint32_t poison = bad ? 0x7fc07fc0u : 0u;
+    const float sam = a.sa[m];
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.residual_out + m * a.ld_res, H * 2u);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        v2u o;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            float y[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float t = u2f(sv[u][2 * k + e]) * u2f(av[u][2 * k + e]);
+                const float b = u2f(e ? (bv[u][k] & 0xffff0000u) : (bv[u][k] << 16));
+                y[e] = hb ? __builtin_fmaf(sam, t, b) : sam * t;
+            }
+            const uint32_t br2 = cvt_bf16x2(y[0], y[1]);                       // the scale pass's rounding
+            const float p0 = u2f(gv[u][k] << 16) * u2f(br2 << 16);
+            const float p1 = u2f(gv[u][k] & 0xffff0000u) * u2f(br2 & 0xffff0000u);
+            o[k] = cvt_bf16x2(u2f(xv[u][k] << 16) + p0, u2f(xv[u][k] & 0xffff0000u) + p1) | poison;
+        }
+        __builtin_amdgcn_raw_buffer_store_b64(o, orr, (g0 + 256u * u) * 8u, 0, 0);
+    }
+}
+
+int launch_indexed_gate(const RmsArgs& a, hipStream_t st) {
+    const int64_t groups = a.H >> 2;
+    const int u = (int)std::min<int64_t>(4, (groups + 255) / 256);
+    const dim3 grid((unsigned)a.M, (unsigned)((groups + 256 * u - 1) / (256 * u))), block(256);
+    if (u <= 1) hipLaunchKernelGGL(scale_indexed_gate_seg_kernel<1>, grid, block, 0, st, a);
+    else if (u == 2) hipLaunchKernelGGL(scale_indexed_gate_seg_kernel<2>, grid, block, 0, st, a);
+    else if (u == 3) hipLaunchKernelGGL(scale_indexed_gate_seg_kernel<3>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(scale_indexed_gate_seg_kernel<4>, grid, block, 0, st, a);
+    H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
 
@@ -466,7 +531,8 @@ int h3fp8_scale_indexed_gate(const float* acc, int64_t ld_acc, const float* sa, 
     H3_REQUIRE(idx_bytes == 4 || idx_bytes == 8, "h3fp8_scale_indexed_gate: indices must be int32 or int64");
     int rc = check_rms(a, true, true, false, "h3fp8_scale_indexed_gate");
     if (rc || M == 0 || H == 0) return rc;
-    return launch_rms<true, 0, true, false>(a, (hipStream_t)stream);
+    H3_REQUIRE(M < ((int64_t)1 << 31), "h3fp8_scale_indexed_gate: too many rows");
+    return launch_indexed_gate(a, (hipStream_t)stream);
 }
 
 }  // extern "C"
