@@ -211,6 +211,7 @@ int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, 
     a.out_q = (uint16_t*)out_q; a.ldq_t = ldq_t; a.ldq_h = ldq_h;
     a.out_k = (uint16_t*)out_k; a.ldk_t = ldk_t; a.ldk_h = ldk_h;
     const int64_t units = T * ((Hq + Hk + 7) / 8);
+    H3_REQUIRE(units < ((int64_t)1 << 33), "h3fp8_scale_qk_norm_rope: too many tokens");
     hipLaunchKernelGGL(scale_qk_norm_rope_kernel, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
                        a, units);
     H3_CHECK_HIP(hipGetLastError());

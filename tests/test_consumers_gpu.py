@@ -124,7 +124,7 @@ def test_gate_rms_matches_oracle(cuda, T, hidden, bias):
     assert_quant_equal(q2, s2, q_ref, s_ref)
 
 
-@pytest.mark.parametrize("T,hidden", [(1, 128), (37, 200), (2000, 3072)])
+@pytest.mark.parametrize("T,hidden", [(1, 128), (37, 200), (2000, 3072), (3, 8), (65, 5376), (9, 8192)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_indexed_gate_matches_oracle(cuda, T, hidden, bias):
     from h3_tp2_amd import fp8_consumers as fc
@@ -140,6 +140,28 @@ def test_indexed_gate_matches_oracle(cuda, T, hidden, bias):
     torch.cuda.synchronize()
     assert out.data_ptr() == st.ph.data_ptr()
     _nan_aware_equal(bits16(out), r_ref, "indexed_gate")
+
+
+def test_indexed_gate_index_out_of_range_poisons_only_its_row(cuda):
+    """fc2's elementwise kernel: an index past the gate table is not read through; that row is NaN, the others exact."""
+    from h3_tp2_amd import ops
+    T, hidden = 12, 1000
+    x32, sa, sb, b = _operands(T, hidden, seed=77, bias=True)
+    x, w, sh, sc, gt, idx = mod_inputs(T, hidden, seed=78, B=3)
+    bad = idx.clone()
+    bad[4] = 3
+    bad[7] = -2
+    gd = gt._base.to(cuda)[:, 2 * hidden:3 * hidden]
+    out = ops.scale_indexed_gate(*_dev(x32, sa, sb, b, cuda=cuda), x.to(cuda), gd, bad.to(cuda))
+    torch.cuda.synchronize()
+    ok = [m for m in range(T) if m not in (4, 7)]
+    branch = _epi(x32, sa, sb, b)
+    r_ref, _, _, _ = O.gate_rms_quant(bits16(x[ok]), bits16(gt), branch[ok], bits16(w), bits16(sh), bits16(sc),
+                                      idx[ok].numpy(), EPS)
+    got = bits16(out)
+    assert np.array_equal(got[ok], r_ref)
+    for m in (4, 7):
+        assert ((got[m] & 0x7FFF) > 0x7F80).all()
 
 
 def test_directed_values_all_consumers(cuda):
