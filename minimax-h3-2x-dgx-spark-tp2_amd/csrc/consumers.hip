@@ -58,6 +58,8 @@ __device__ __forceinline__ float hi_bf16(uint32_t w) { return u2f(w & 0xffff0000
 // Lane k of a head holds dims 32 i + 4 k + e (chunk i = 0 .. 3, e = 0 .. 3): one 16-byte load instruction covers a
 // head's 128 contiguous bytes of the product, so the loads coalesce.  The rotation partner of every rotated dim is lane
 // k ^ 4; which of its chunks it is depends on the side of the lane (k < 4 or k >= 4) -- the sender picks it.
+// HB: a bias is given; RF: the rope table is fp32 (else bf16).
+template <bool HB, bool RF>
 __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64_t units) {
     const int lane = threadIdx.x & 63;
     const int k = lane & 7;
@@ -82,7 +84,7 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
     uint2 bw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        bw[i] = a.bias ? *reinterpret_cast<const uint2*>(a.bias + c + 32 * i) : make_uint2(0u, 0u);
+        bw[i] = HB ? *reinterpret_cast<const uint2*>(a.bias + c + 32 * i) : make_uint2(0u, 0u);
     const uint16_t* wp = (isq ? a.wq : a.wk) + 4 * k;
     uint2 wb[4];
 #pragma unroll
@@ -92,7 +94,7 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
     //   chunk 2: dims 64 + 4k + e >= 48, fd = 16 + 4k
     const int fdi[3] = {4 * k, up ? 4 * k - 16 : 32 + 4 * k, 16 + 4 * k};
     v4u cr[3], sr[3];
-    if (a.rope_f32) {
+    if (RF) {
         const float* rr = reinterpret_cast<const float*>(a.rope) + t * a.ld_rope;
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
@@ -117,7 +119,7 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float p = sv[i][e] * av[i][e];
-            if (a.bias) {
+            if (HB) {
                 const uint32_t bb = (e >> 1) ? bw[i].y : bw[i].x;
                 x[4 * i + e] = __builtin_fmaf(sam, p, (e & 1) ? hi_bf16(bb) : lo_bf16(bb));
             } else {
@@ -147,15 +149,18 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
     // the partner chunk of target chunk i: lanes k < 4 take chunk (i + 1) % 3 of lane k + 4, lanes k >= 4 chunk
     // (i + 2) % 3 of lane k - 4, so lane k sends chunk (i + 1) % 3 if k >= 4 and (i + 2) % 3 if k < 4
     uint32_t ob[8];
+    const uint32_t upmask = up ? 0xffffffffu : 0u;
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int cu = (i + 1) % 3, cl = (i + 2) % 3;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            const uint32_t send = up ? nb[2 * cu + q] : nb[2 * cl + q];
+            // constant indices on both sides, merged by a bit select (a select of the index would become a
+            // chain of compares over all eight registers)
+            const uint32_t send = (nb[2 * cu + q] & upmask) | (nb[2 * cl + q] & ~upmask);
             const uint32_t pb = (uint32_t)__shfl_xor((int)send, 4, 64);
             float cs[2], sn[2];
-            if (a.rope_f32) {
+            if (RF) {
                 cs[0] = u2f(cr[i][2 * q]); cs[1] = u2f(cr[i][2 * q + 1]);
                 sn[0] = u2f(sr[i][2 * q]); sn[1] = u2f(sr[i][2 * q + 1]);
             } else {
@@ -212,8 +217,12 @@ int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, 
     a.out_k = (uint16_t*)out_k; a.ldk_t = ldk_t; a.ldk_h = ldk_h;
     const int64_t units = T * ((Hq + Hk + 7) / 8);
     H3_REQUIRE(units < ((int64_t)1 << 33), "h3fp8_scale_qk_norm_rope: too many tokens");
-    hipLaunchKernelGGL(scale_qk_norm_rope_kernel, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
-                       a, units);
+    const dim3 grid((unsigned)((units + 3) / 4)), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    if (a.bias && a.rope_f32) hipLaunchKernelGGL((scale_qk_norm_rope_kernel<true, true>), grid, block, 0, st, a, units);
+    else if (a.bias) hipLaunchKernelGGL((scale_qk_norm_rope_kernel<true, false>), grid, block, 0, st, a, units);
+    else if (a.rope_f32) hipLaunchKernelGGL((scale_qk_norm_rope_kernel<false, true>), grid, block, 0, st, a, units);
+    else hipLaunchKernelGGL((scale_qk_norm_rope_kernel<false, false>), grid, block, 0, st, a, units);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
