@@ -287,3 +287,39 @@ def test_consumer_wrappers_take_the_stash_after_the_selfcheck(cuda, monkeypatch)
     s = fc.stats()
     assert (s["fused_out"], s["fused_fc2"], s["fused_qkv"], s["selfcheck_fail"]) == (1, 1, 1, 0), s
     assert s["selfcheck_pass"] == 3 and s["materialize"] == 0
+
+
+def test_full_size_qkv_consumer(cuda):
+    """The qkv consumer at the benchmark's token count (T = 16740, 24 q + 24 k heads of 128 and the v columns' scale
+    pass, fp32 rope table), against the oracle."""
+    from h3_tp2_amd import fp8_consumers as fc
+    T, H, D = 16740, 24, 128
+    N = 3 * H * D
+    x32, sa, sb, b = _operands(T, N, seed=2024, bias=True)
+    g = torch.Generator().manual_seed(11)
+    wq = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    wk = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    rope = rope_table(T, torch.float32)
+    st = fc.Stash(*_dev(x32, sa, sb, b, cuda=cuda), torch.empty((T, N), dtype=BF16, device=cuda))
+    oq, ok, v = fc.qk_norm_rope_fused(st, H, H, D, wq.to(cuda), wk.to(cuda), rope.to(cuda), EPS)
+    torch.cuda.synchronize()
+    p = _epi(x32, sa, sb, b)
+    tab = rope.numpy()
+    _nan_aware_equal(bits16(oq), O.qk_norm_rope(p[:, :H * D].reshape(T, H, D), bits16(wq), tab, EPS), "q")
+    _nan_aware_equal(bits16(ok), O.qk_norm_rope(p[:, H * D:2 * H * D].reshape(T, H, D), bits16(wk), tab, EPS), "k")
+    assert np.array_equal(bits16(v), p[:, 2 * H * D:].reshape(T, H, D))
+
+
+def test_full_size_fc2_consumer(cuda):
+    """fc2's indexed_gate at the benchmark's 1344x768 5 s token count (31248 rows of 3072), against the oracle."""
+    from h3_tp2_amd import ops
+    T, hidden = 31248, 3072
+    x32, sa, sb, b = _operands(T, hidden, seed=2025, bias=False)
+    x, w, sh, sc, gt, idx = mod_inputs(T, hidden, seed=2026, B=6)
+    gd = gt._base.to(cuda)[:, 2 * hidden:3 * hidden]
+    out = ops.scale_indexed_gate(*_dev(x32, sa, sb, b, cuda=cuda), x.to(cuda), gd, idx.to(cuda))
+    torch.cuda.synchronize()
+    branch = _epi(x32, sa, sb, b)
+    r_ref, _, _, _ = O.gate_rms_quant(bits16(x), bits16(gt), branch, bits16(w), bits16(sh), bits16(sc), idx.numpy(),
+                                      EPS)
+    _nan_aware_equal(bits16(out), r_ref, "indexed_gate")
