@@ -249,7 +249,17 @@ def main() -> None:
             xs.append(xg)
         t = time_steps(lambda: ops.grouped_gemm(probs), steps, warm) / steps
         f5 = sum(2.0 * Mg * Ng * Kg for Mg, Kg, Ng, _ in groups)
-        out["c5_grouped_one_launch"] = {"ms": round(t, 4), "TFLOP/s": round(f5 / (t * 1e-3) / 1e12, 1)}
+        out["c5_grouped_one_launch"] = {"ms": round(t, 4), "TFLOP/s": round(f5 / (t * 1e-3) / 1e12, 1),
+                                        "note": "all four groups' FLOPs counted, the M=2 adaLN group's included"}
+        # the M=2 adaLN group alone: bound by reading its fp8 weight (N x K bytes), reported in GB/s
+        Mg, Kg, Ng, _ = groups[0]
+        qa, wa, sqa, swa = probs[0]
+        t2 = time_steps(lambda: ops.gemm(qa, wa, sqa, swa, torch.bfloat16), steps, warm) / steps
+        wbytes = float(Ng * Kg)
+        out["c5_grouped_one_launch"]["adaLN_M2_alone"] = {
+            "ms": round(t2, 4), "GB/s": round(wbytes / (t2 * 1e-3) / 1e9, 1),
+            "frac_hbm": round(wbytes / (t2 * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "form": f"kernel 2 on [{Mg},{Kg}] x [{Ng},{Kg}]: {Ng // 256} column tiles of 256 x 256 run as half tiles"}
         del probs, xs
 
     if want("producers"):
