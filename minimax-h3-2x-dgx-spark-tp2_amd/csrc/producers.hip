@@ -126,7 +126,7 @@ __device__ __forceinline__ v4u tab16(const GlobalTables& t, int which, int c) {
 // row's instead of following the reduction); above 8 chunks per lane (6 for the fp32-branch form) the registers do
 // not allow it.
 // `tables(bad)` returns the row's table source and sets `bad` (index out of range); it is called after the row's own
-// loads are issued, so the index load and the table loads that depend on it overlap the row's latency.
+// loads are issued, so the table loads that depend on the index overlap the row's latency.
 //
 // B32 (gate form only): the branch is the scaled-GEMM epilogue of the fp32 product `acc` (the consumer of the out
 // projection reading the accumulator instead of a bf16 output).
@@ -302,8 +302,12 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     const int lane = threadIdx.x & 63;
     const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (m >= a.M) return;
+    // the row's index is read first (a scalar load): its latency then overlaps the issue of the row's own loads
+    bool bad0;
+    const int64_t i0 = row_index(a, m, bad0);
     rms_mod_quant_row<GATE, OUT, CPL, (CPL <= 6 || (CPL <= 8 && !B32)), B32, FULL>(a, m, lane, [&](bool& bad) {
-        const int64_t i = row_index(a, m, bad);
+        bad = bad0;
+        const int64_t i = i0;
         const uint32_t rb = (uint32_t)a.H * 2u;
         GlobalTables t;
         t.w = make_rsrc(a.weight, rb);
