@@ -380,8 +380,8 @@ int check_rms(const RmsArgs& a, bool gate, bool b32, bool norm, const char* who)
 // indexed_gate of the fc2 site reading the fp32 product: out = bf16(x + gate[i] * branch), branch = the scale pass's
 // bf16(sa * (sb * acc)) (or its fma with the bias) -- elementwise, so no row needs to stay in registers.  Block (m, s)
 // covers U * 256 groups of 4 columns of row m, thread t the groups t + 256 u (coalesced per u).  Every access is a
-// range-checked buffer load or store (groups past the row read zero and are not written); the row's own loads go out
-// before the index, the gate row's after it.  An index outside the table reads gate row 0 and writes NaN.
+// range-checked buffer load or store (groups past the row read zero and are not written); the index is read first,
+// the gate row's loads go out after the row's own.  An index outside the table reads gate row 0 and writes NaN.
 template <int U>
 __global__ void __launch_bounds__(256) scale_indexed_gate_seg_kernel(RmsArgs a) {
     const int64_t m = blockIdx.x;
@@ -392,6 +392,8 @@ __global__ void __launch_bounds__(256) scale_indexed_gate_seg_kernel(RmsArgs a) 
     const bool hb = a.bias != nullptr;
     const __amdgpu_buffer_rsrc_t br = make_rsrc(hb ? (const void*)a.bias : (const void*)a.sb, hb ? H * 2u : 0u);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + m * a.ldx, H * 2u);
+    bool bad;
+    const int64_t i = row_index(a, m, bad);                // a scalar load, in flight with the row's loads
     v4u av[U], sv[U];
     v2u bv[U], xv[U], gv[U];
 #pragma unroll
@@ -402,8 +404,6 @@ __global__ void __launch_bounds__(256) scale_indexed_gate_seg_kernel(RmsArgs a) 
         sv[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, g * 16u, 0, 0);
         bv[u] = __builtin_amdgcn_raw_buffer_load_b64(br, g * 8u, 0, 0);       // zeros without a bias
     }
-    bool bad;
-    const int64_t i = row_index(a, m, bad);
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gate + i * a.ld_gate, H * 2u);
 #pragma unroll
     for (int u = 0; u < U; ++u) gv[u] = __builtin_amdgcn_raw_buffer_load_b64(gr, (g0 + 256u * u) * 8u, 0, 0);
