@@ -14,8 +14,9 @@
 //
 // A unit is one token's group of 8 heads, one 64-lane wave: lanes 8j .. 8j + 7 hold head 8g + j, lane k of the eight
 // dims 32i + 4k .. 32i + 4k + 3 for i = 0 .. 3 (16 dims per lane, so the per-head work -- the butterfly, the two
-// divisions, the square root -- is shared by 16 dims), 4 waves per 256-thread workgroup, one unit each.  The v columns of the product go through the plain scale pass (h3fp8_scale_bias_cast) into
-// the placeholder, where the attention reads them.
+// divisions, the square root -- is shared by 16 dims), 4 waves per 256-thread workgroup, one unit each.  The v
+// columns of the product go through the plain scale pass (h3fp8_scale_bias_cast) into the placeholder, where the
+// attention reads them.
 #include "h3fp8_common.h"
 
 namespace {
