@@ -273,43 +273,56 @@ __global__ void __launch_bounds__(256) scale_bias_cast_kernel(const float* __res
     *reinterpret_cast<uint2*>(y + m * ldy + n) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
 }
 
-// The scale pass over row segments, for contiguous (16-byte aligned) sb and an 8-byte aligned bias: block (m, s) covers
-// the U * 256 column groups of segment s of row m, thread i the groups i + 256 u (coalesced per u).  Every load is a
-// range-checked buffer load (groups past the row read zero and their stores are dropped), so all U groups' loads are
-// in flight before the first use; no per-thread division.
+// The scale pass over row segments, for contiguous (16-byte aligned) sb and an 8-byte aligned bias: block (b, s) covers
+// the U * 256 column groups of segment s of rows 2b and 2b + 1, thread i the groups i + 256 u (coalesced per u); the
+// two rows share the segment's sb / bias loads.  Every load is a range-checked buffer load (groups past the row, and a
+// second row past M, read zero; stores past the row are dropped), so all of a thread's loads are in flight before the
+// first use; no per-thread division.
 template <int OUT_DT, int U>
 __global__ void __launch_bounds__(256) scale_bias_cast_seg_kernel(const float* __restrict__ x, int64_t ldx, int64_t N,
-                                                                  EpiArgs e, uint16_t* __restrict__ y, int64_t ldy) {
-    const int64_t m = blockIdx.x;
+                                                                  EpiArgs e, uint16_t* __restrict__ y, int64_t ldy,
+                                                                  int64_t M) {
+    constexpr int R = 2;
+    const int64_t m0 = (int64_t)blockIdx.x * R;
     const uint32_t g0 = blockIdx.y * (256u * U) + threadIdx.x;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + m * ldx, (uint32_t)N * 4u);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(e.sb, (uint32_t)N * 4u);
     const bool hb = e.bias != nullptr;
     const __amdgpu_buffer_rsrc_t br = make_rsrc(hb ? (const void*)e.bias : (const void*)e.sb, hb ? (uint32_t)N * 2u : 0u);
-    const __amdgpu_buffer_rsrc_t yr = make_rsrc(y + m * ldy, (uint32_t)N * 2u);
-    v4u xv[U], sv[U];
+    v4u xv[R][U], sv[U];
     v2u bv[U];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const bool in = m0 + r < M;
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + (in ? m0 + r : m0) * ldx, in ? (uint32_t)N * 4u : 0u);
+#pragma unroll
+        for (int u = 0; u < U; ++u) xv[r][u] = __builtin_amdgcn_raw_buffer_load_b128(xr, (g0 + 256u * u) * 16u, 0, 2);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint32_t g = g0 + 256u * u;
-        xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, g * 16u, 0, 2);     // streamed once: non-temporal
         sv[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, g * 16u, 0, 0);
         bv[u] = __builtin_amdgcn_raw_buffer_load_b64(br, g * 8u, 0, 0);        // zeros without a bias
     }
-    const float sam = e.sa[m * e.sa_stride];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        uint32_t o[4];
+    for (int r = 0; r < R; ++r) {
+        const int64_t m = m0 + r;
+        if (m >= M) break;
+        const float sam = e.sa[m * e.sa_stride];
+        const __amdgpu_buffer_rsrc_t yr = make_rsrc(y + m * ldy, (uint32_t)N * 2u);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t bw = bv[u][r >> 1];
-            const uint32_t bh = (r & 1) ? (bw >> 16) : (bw & 0xffffu);
-            const float b = OUT_DT ? fp16_to_f32(bh) : bf16_to_f32(bh);
-            const float val = epi(u2f(xv[u][r]), sam, u2f(sv[u][r]), hb, b);
-            o[r] = OUT_DT ? fp16_rne(val) : bf16_rne(val);
+        for (int u = 0; u < U; ++u) {
+            uint32_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t bw = bv[u][q >> 1];
+                const uint32_t bh = (q & 1) ? (bw >> 16) : (bw & 0xffffu);
+                const float b = OUT_DT ? fp16_to_f32(bh) : bf16_to_f32(bh);
+                const float val = epi(u2f(xv[r][u][q]), sam, u2f(sv[u][q]), hb, b);
+                o[q] = OUT_DT ? fp16_rne(val) : bf16_rne(val);
+            }
+            const v2u ov = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+            __builtin_amdgcn_raw_buffer_store_b64(ov, yr, (g0 + 256u * u) * 8u, 0, 0);
         }
-        const v2u ov = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
-        __builtin_amdgcn_raw_buffer_store_b64(ov, yr, (g0 + 256u * u) * 8u, 0, 0);
     }
 }
 
@@ -318,11 +331,11 @@ void launch_scale_bias_cast_seg(const float* x, int64_t ldx, int64_t M, int64_t 
                                 int64_t ldy, hipStream_t st) {
     const int64_t groups = N >> 2;
     const int u = (int)std::min<int64_t>(4, (groups + 255) / 256);
-    dim3 grid((unsigned)M, (unsigned)((groups + 256 * u - 1) / (256 * u))), block(256);
-    if (u <= 1) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 1>), grid, block, 0, st, x, ldx, N, e, y, ldy);
-    else if (u == 2) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 2>), grid, block, 0, st, x, ldx, N, e, y, ldy);
-    else if (u == 3) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 3>), grid, block, 0, st, x, ldx, N, e, y, ldy);
-    else hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 4>), grid, block, 0, st, x, ldx, N, e, y, ldy);
+    dim3 grid((unsigned)((M + 1) / 2), (unsigned)((groups + 256 * u - 1) / (256 * u))), block(256);
+    if (u <= 1) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 1>), grid, block, 0, st, x, ldx, N, e, y, ldy, M);
+    else if (u == 2) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 2>), grid, block, 0, st, x, ldx, N, e, y, ldy, M);
+    else if (u == 3) hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 3>), grid, block, 0, st, x, ldx, N, e, y, ldy, M);
+    else hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 4>), grid, block, 0, st, x, ldx, N, e, y, ldy, M);
 }
 
 // The persistent LDS-table form of the bf16-source pass, when its 16-byte loads and 8-byte stores are aligned and a row
