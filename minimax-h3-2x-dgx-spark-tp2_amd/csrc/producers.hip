@@ -378,63 +378,84 @@ int check_rms(const RmsArgs& a, bool gate, bool b32, bool norm, const char* who)
 }
 
 // indexed_gate of the fc2 site reading the fp32 product: out = bf16(x + gate[i] * branch), branch = the scale pass's
-// bf16(sa * (sb * acc)) (or its fma with the bias) -- elementwise, so no row needs to stay in registers.  Block (m, s)
-// covers U * 256 groups of 4 columns of row m, thread t the groups t + 256 u (coalesced per u).  Every access is a
-// range-checked buffer load or store (groups past the row read zero and are not written); the index is read first,
-// the gate row's loads go out after the row's own.  An index outside the table reads gate row 0 and writes NaN.
+// bf16(sa * (sb * acc)) (or its fma with the bias) -- elementwise, so no row needs to stay in registers.  Block (b, s)
+// covers U * 256 groups of 4 columns of rows 2b and 2b + 1, thread t the groups t + 256 u (coalesced per u); the two
+// rows share the segment's sb / bias loads.  Every access is a range-checked buffer load or store (groups past the
+// row, and a second row past M, read zero; stores past the row are dropped); the two indices are read first, the gate
+// rows' loads go out after the rows' own.  An index outside the table reads gate row 0 and writes NaN.
 template <int U>
 __global__ void __launch_bounds__(256) scale_indexed_gate_seg_kernel(RmsArgs a) {
-    const int64_t m = blockIdx.x;
+    constexpr int R = 2;
+    const int64_t m0 = (int64_t)blockIdx.x * R;
     const uint32_t g0 = blockIdx.y * (256u * U) + threadIdx.x;
     const uint32_t H = (uint32_t)a.H;
-    const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.acc + m * a.ld_acc, H * 4u);
+    bool bad[R];
+    int64_t idx[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) idx[r] = row_index(a, m0 + r < a.M ? m0 + r : m0, bad[r]);   // scalar loads first
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sb, H * 4u);
     const bool hb = a.bias != nullptr;
     const __amdgpu_buffer_rsrc_t br = make_rsrc(hb ? (const void*)a.bias : (const void*)a.sb, hb ? H * 2u : 0u);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + m * a.ldx, H * 2u);
-    bool bad;
-    const int64_t i = row_index(a, m, bad);                // a scalar load, in flight with the row's loads
-    v4u av[U], sv[U];
-    v2u bv[U], xv[U], gv[U];
+    v4u av[R][U], sv[U];
+    v2u bv[U], xv[R][U], gv[R][U];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const bool in = m0 + r < a.M;
+        const int64_t m = in ? m0 + r : m0;
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.acc + m * a.ld_acc, in ? H * 4u : 0u);
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + m * a.ldx, in ? H * 2u : 0u);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t g = g0 + 256u * u;
+            av[r][u] = __builtin_amdgcn_raw_buffer_load_b128(ar, g * 16u, 0, 2);    // streamed once: non-temporal
+            xv[r][u] = __builtin_amdgcn_raw_buffer_load_b64(xr, g * 8u, 0, 2);
+        }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint32_t g = g0 + 256u * u;
-        av[u] = __builtin_amdgcn_raw_buffer_load_b128(ar, g * 16u, 0, 2);    // streamed once: non-temporal
-        xv[u] = __builtin_amdgcn_raw_buffer_load_b64(xr, g * 8u, 0, 2);
         sv[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, g * 16u, 0, 0);
         bv[u] = __builtin_amdgcn_raw_buffer_load_b64(br, g * 8u, 0, 0);       // zeros without a bias
     }
-    const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gate + i * a.ld_gate, H * 2u);
 #pragma unroll
-    for (int u = 0; u < U; ++u) gv[u] = __builtin_amdgcn_raw_buffer_load_b64(gr, (g0 + 256u * u) * 8u, 0, 0);
-    const uint32_t poison = bad ? 0x7fc07fc0u : 0u;
-    const float sam = a.sa[m];
-    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.residual_out + m * a.ld_res, H * 2u);
+    for (int r = 0; r < R; ++r) {
+        const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gate + idx[r] * a.ld_gate, H * 2u);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        v2u o;
+        for (int u = 0; u < U; ++u) gv[r][u] = __builtin_amdgcn_raw_buffer_load_b64(gr, (g0 + 256u * u) * 8u, 0, 0);
+    }
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            float y[2];
+    for (int r = 0; r < R; ++r) {
+        const int64_t m = m0 + r;
+        if (m >= a.M) break;
+        const uint32_t poison = bad[r] ? 0x7fc07fc0u : 0u;
+        const float sam = a.sa[m];
+        const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.residual_out + m * a.ld_res, H * 2u);
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const float t = u2f(sv[u][2 * k + e]) * u2f(av[u][2 * k + e]);
-                const float b = u2f(e ? (bv[u][k] & 0xffff0000u) : (bv[u][k] << 16));
-                y[e] = hb ? __builtin_fmaf(sam, t, b) : sam * t;
+        for (int u = 0; u < U; ++u) {
+            v2u o;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                float y[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float t = u2f(sv[u][2 * k + e]) * u2f(av[r][u][2 * k + e]);
+                    const float b = u2f(e ? (bv[u][k] & 0xffff0000u) : (bv[u][k] << 16));
+                    y[e] = hb ? __builtin_fmaf(sam, t, b) : sam * t;
+                }
+                const uint32_t br2 = cvt_bf16x2(y[0], y[1]);                   // the scale pass's rounding
+                const float p0 = u2f(gv[r][u][k] << 16) * u2f(br2 << 16);
+                const float p1 = u2f(gv[r][u][k] & 0xffff0000u) * u2f(br2 & 0xffff0000u);
+                o[k] = cvt_bf16x2(u2f(xv[r][u][k] << 16) + p0, u2f(xv[r][u][k] & 0xffff0000u) + p1) | poison;
             }
-            const uint32_t br2 = cvt_bf16x2(y[0], y[1]);                       // the scale pass's rounding
-            const float p0 = u2f(gv[u][k] << 16) * u2f(br2 << 16);
-            const float p1 = u2f(gv[u][k] & 0xffff0000u) * u2f(br2 & 0xffff0000u);
-            o[k] = cvt_bf16x2(u2f(xv[u][k] << 16) + p0, u2f(xv[u][k] & 0xffff0000u) + p1) | poison;
+            __builtin_amdgcn_raw_buffer_store_b64(o, orr, (g0 + 256u * u) * 8u, 0, 0);
         }
-        __builtin_amdgcn_raw_buffer_store_b64(o, orr, (g0 + 256u * u) * 8u, 0, 0);
     }
 }
 
 int launch_indexed_gate(const RmsArgs& a, hipStream_t st) {
     const int64_t groups = a.H >> 2;
     const int u = (int)std::min<int64_t>(4, (groups + 255) / 256);
-    const dim3 grid((unsigned)a.M, (unsigned)((groups + 256 * u - 1) / (256 * u))), block(256);
+    const dim3 grid((unsigned)((a.M + 1) / 2), (unsigned)((groups + 256 * u - 1) / (256 * u))), block(256);
     if (u <= 1) hipLaunchKernelGGL(scale_indexed_gate_seg_kernel<1>, grid, block, 0, st, a);
     else if (u == 2) hipLaunchKernelGGL(scale_indexed_gate_seg_kernel<2>, grid, block, 0, st, a);
     else if (u == 3) hipLaunchKernelGGL(scale_indexed_gate_seg_kernel<3>, grid, block, 0, st, a);
