@@ -12,9 +12,9 @@
 //           bf16(n_d * cos + n_(d-48) * sin)   48 <= d < 96, cos / sin = rope[t, d - 48], rope[t, d]
 //           n_d                                 d >= 96
 //
-// A unit is one token's group of 8 heads, one 64-lane wave: lanes 8j .. 8j + 7 hold head 8g + j, lane k of the eight
-// dims 32i + 4k .. 32i + 4k + 3 for i = 0 .. 3 (16 dims per lane, so the per-head work -- the butterfly, the two
-// divisions, the square root -- is shared by 16 dims), 4 waves per 256-thread workgroup, one unit each.  The v
+// A 64-lane wave takes a group of 8 heads of two consecutive tokens: lanes 8j .. 8j + 7 hold head 8g + j, lane k of
+// the eight dims 32i + 4k .. 32i + 4k + 3 for i = 0 .. 3 (16 dims per lane, so the per-head work -- the butterfly, the
+// two divisions, the square root -- is shared by 16 dims), 4 waves per 256-thread workgroup.  The v
 // columns of the product go through the plain scale pass (h3fp8_scale_bias_cast) into the placeholder, where the
 // attention reads them.
 #include "h3fp8_common.h"
@@ -60,47 +60,51 @@ __device__ __forceinline__ float hi_bf16(uint32_t w) { return u2f(w & 0xffff0000
 // head's 128 contiguous bytes of the product, so the loads coalesce.  The rotation partner of every rotated dim is lane
 // k ^ 4; which of its chunks it is depends on the side of the lane (k < 4 or k >= 4) -- the sender picks it.
 // HB: a bias is given; RF: the rope table is fp32 (else bf16).
+//
+// Everything one token's group of 8 heads reads (the lane's share), loaded before any of it is used.
+struct QkIn {
+    v4f av[4], sv[4];
+    uint2 bw[4], wb[4];
+    v4u cr[3], sr[3];
+    float sam;
+    int64_t t;
+    int h;
+};
+
 template <bool HB, bool RF>
-__global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64_t units) {
-    const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void qk_load(const QkArgs& a, int64_t t, int g, int lane, QkIn& L) {
     const int k = lane & 7;
     const bool up = k >= 4;
     const int heads = a.Hq + a.Hk;
-    const int groups = (heads + 7) / 8;
-    const int64_t w = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (w >= units) return;
-    const int64_t t = w / groups;
-    const int h = 8 * (int)(w - t * groups) + (lane >> 3);
+    const int h = 8 * g + (lane >> 3);
     const bool live = h < heads;                                 // the last group of a head count not divisible by 8
     const bool isq = h < a.Hq;
+    L.t = t;
+    L.h = h;
     const int64_t c = (int64_t)(live ? h : 0) * 128 + 4 * k;     // product column of the lane's dim 4k (chunk 0)
     // every load first: 4 x 16 B of the product and of sb, 4 x 8 B of bias and weight, the rope entries (bf16 operands
     // in 8-byte pieces: they need only 8-byte alignment)
     const float* ap = a.acc + t * a.ld_acc + c;
-    v4f av[4], sv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) av[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(ap + 32 * i));
+    for (int i = 0; i < 4; ++i) L.av[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(ap + 32 * i));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sv[i] = *reinterpret_cast<const v4f*>(a.sb + c + 32 * i);
-    uint2 bw[4];
+    for (int i = 0; i < 4; ++i) L.sv[i] = *reinterpret_cast<const v4f*>(a.sb + c + 32 * i);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        bw[i] = HB ? *reinterpret_cast<const uint2*>(a.bias + c + 32 * i) : make_uint2(0u, 0u);
+        L.bw[i] = HB ? *reinterpret_cast<const uint2*>(a.bias + c + 32 * i) : make_uint2(0u, 0u);
     const uint16_t* wp = (isq ? a.wq : a.wk) + 4 * k;
-    uint2 wb[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wb[i] = *reinterpret_cast<const uint2*>(wp + 32 * i);
+    for (int i = 0; i < 4; ++i) L.wb[i] = *reinterpret_cast<const uint2*>(wp + 32 * i);
     // rope entries of the rotated chunks 0 .. 2: cos at table index fd, sin at fd + 48
     //   chunk 0: dims 4k + e < 48, fd = 4k;  chunk 1: dims 32 + 4k + e, fd = 32 + 4k (k < 4) or 4k - 16 (k >= 4);
     //   chunk 2: dims 64 + 4k + e >= 48, fd = 16 + 4k
     const int fdi[3] = {4 * k, up ? 4 * k - 16 : 32 + 4 * k, 16 + 4 * k};
-    v4u cr[3], sr[3];
     if (RF) {
         const float* rr = reinterpret_cast<const float*>(a.rope) + t * a.ld_rope;
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            cr[i] = *reinterpret_cast<const v4u*>(rr + fdi[i]);
-            sr[i] = *reinterpret_cast<const v4u*>(rr + fdi[i] + 48);
+            L.cr[i] = *reinterpret_cast<const v4u*>(rr + fdi[i]);
+            L.sr[i] = *reinterpret_cast<const v4u*>(rr + fdi[i] + 48);
         }
     } else {
         const uint16_t* rr = reinterpret_cast<const uint16_t*>(a.rope) + t * a.ld_rope;
@@ -108,23 +112,33 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
         for (int i = 0; i < 3; ++i) {
             const uint2 cw = *reinterpret_cast<const uint2*>(rr + fdi[i]);
             const uint2 sw = *reinterpret_cast<const uint2*>(rr + fdi[i] + 48);
-            cr[i] = v4u{cw.x, cw.y, 0u, 0u};
-            sr[i] = v4u{sw.x, sw.y, 0u, 0u};
+            L.cr[i] = v4u{cw.x, cw.y, 0u, 0u};
+            L.sr[i] = v4u{sw.x, sw.y, 0u, 0u};
         }
     }
-    const float sam = a.sa[t];
+    L.sam = a.sa[t];
+}
+
+template <bool HB, bool RF>
+__device__ __forceinline__ void qk_compute(const QkArgs& a, const QkIn& L, int lane, bool store) {
+    const int k = lane & 7;
+    const bool up = k >= 4;
+    const int64_t t = L.t;
+    const int h = L.h;
+    const bool live = h < a.Hq + a.Hk;
+    const bool isq = h < a.Hq;
     // the scale pass, rounded once to bf16; x[4i + e] is dim 32i + 4k + e
     float x[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float p = sv[i][e] * av[i][e];
+            const float p = L.sv[i][e] * L.av[i][e];
             if (HB) {
-                const uint32_t bb = (e >> 1) ? bw[i].y : bw[i].x;
-                x[4 * i + e] = __builtin_fmaf(sam, p, (e & 1) ? hi_bf16(bb) : lo_bf16(bb));
+                const uint32_t bb = (e >> 1) ? L.bw[i].y : L.bw[i].x;
+                x[4 * i + e] = __builtin_fmaf(L.sam, p, (e & 1) ? hi_bf16(bb) : lo_bf16(bb));
             } else {
-                x[4 * i + e] = sam * p;
+                x[4 * i + e] = L.sam * p;
             }
         }
 #pragma unroll
@@ -144,7 +158,7 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
     uint32_t nb[8];                                              // packed pairs: nb[2i], nb[2i + 1] = chunk i
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const uint32_t ww = (j & 1) ? wb[j >> 1].y : wb[j >> 1].x;
+        const uint32_t ww = (j & 1) ? L.wb[j >> 1].y : L.wb[j >> 1].x;
         nb[j] = cvt_bf16x2((x[2 * j] * r) * lo_bf16(ww), (x[2 * j + 1] * r) * hi_bf16(ww));
     }
     // the partner chunk of target chunk i: lanes k < 4 take chunk (i + 1) % 3 of lane k + 4, lanes k >= 4 chunk
@@ -162,11 +176,11 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
             const uint32_t pb = (uint32_t)__shfl_xor((int)send, 4, 64);
             float cs[2], sn[2];
             if (RF) {
-                cs[0] = u2f(cr[i][2 * q]); cs[1] = u2f(cr[i][2 * q + 1]);
-                sn[0] = u2f(sr[i][2 * q]); sn[1] = u2f(sr[i][2 * q + 1]);
+                cs[0] = u2f(L.cr[i][2 * q]); cs[1] = u2f(L.cr[i][2 * q + 1]);
+                sn[0] = u2f(L.sr[i][2 * q]); sn[1] = u2f(L.sr[i][2 * q + 1]);
             } else {
-                cs[0] = lo_bf16(cr[i][q]); cs[1] = hi_bf16(cr[i][q]);
-                sn[0] = lo_bf16(sr[i][q]); sn[1] = hi_bf16(sr[i][q]);
+                cs[0] = lo_bf16(L.cr[i][q]); cs[1] = hi_bf16(L.cr[i][q]);
+                sn[0] = lo_bf16(L.sr[i][q]); sn[1] = hi_bf16(L.sr[i][q]);
             }
             const uint32_t n = nb[2 * i + q];
             const float u0 = lo_bf16(n) * cs[0], v0 = lo_bf16(pb) * sn[0];
@@ -177,11 +191,30 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
     }
     ob[6] = nb[6];                                               // chunk 3: dims 96 + 4k + e, not rotated
     ob[7] = nb[7];
-    if (!live) return;
+    if (!store || !live) return;
     uint16_t* out = (isq ? a.out_q + t * a.ldq_t + (int64_t)h * a.ldq_h
                          : a.out_k + t * a.ldk_t + (int64_t)(h - a.Hq) * a.ldk_h) + 4 * k;
 #pragma unroll
     for (int i = 0; i < 4; ++i) *reinterpret_cast<uint2*>(out + 32 * i) = make_uint2(ob[2 * i], ob[2 * i + 1]);
+}
+
+// A wave takes head group g of two consecutive tokens: both tokens' loads are issued before either is computed, and
+// the loads that do not depend on the token (sb, bias, norm weights: the same addresses) are issued once.  An odd
+// token count leaves the last wave's second token a copy of its first, not stored.
+template <bool HB, bool RF>
+__global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64_t units) {
+    const int lane = threadIdx.x & 63;
+    const int groups = (a.Hq + a.Hk + 7) / 8;
+    const int64_t w = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (w >= units) return;
+    const int64_t tp = w / groups;
+    const int g = (int)(w - tp * groups);
+    const int64_t t0 = 2 * tp, t1 = t0 + 1 < a.T ? t0 + 1 : t0;
+    QkIn L0, L1;
+    qk_load<HB, RF>(a, t0, g, lane, L0);
+    qk_load<HB, RF>(a, t1, g, lane, L1);
+    qk_compute<HB, RF>(a, L0, lane, true);
+    qk_compute<HB, RF>(a, L1, lane, t0 + 1 < a.T);
 }
 
 }  // namespace
@@ -216,7 +249,7 @@ int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, 
     a.rope = rope; a.ld_rope = ld_rope; a.rope_f32 = rope_f32 ? 1 : 0; a.eps = eps;
     a.out_q = (uint16_t*)out_q; a.ldq_t = ldq_t; a.ldq_h = ldq_h;
     a.out_k = (uint16_t*)out_k; a.ldk_t = ldk_t; a.ldk_h = ldk_h;
-    const int64_t units = T * ((Hq + Hk + 7) / 8);
+    const int64_t units = ((T + 1) / 2) * ((Hq + Hk + 7) / 8);
     H3_REQUIRE(units < ((int64_t)1 << 33), "h3fp8_scale_qk_norm_rope: too many tokens");
     const dim3 grid((unsigned)((units + 3) / 4)), block(256);
     hipStream_t st = (hipStream_t)stream;
