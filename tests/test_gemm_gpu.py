@@ -181,3 +181,23 @@ def test_half_tile_tail_equals_full_tiles(cuda, M, N, K):
     torch.cuda.synchronize()
     assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
     assert_quant_equal(q, s, *oracle_quant(y2.cpu()))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4352, 128), (4100, 4368, 64), (5000, 2560, 64), (2300, 3600, 192),
+                                   (1000, 3008, 96), (6000, 2816, 48)])
+def test_integer_inputs_exact_launch_splits(cuda, M, N, K):
+    """Shapes whose tile counts take each launch form on 256 CUs: whole rounds plus a half-tile tail (272, 306 and 264
+    tiles), full tiles only (200 and 135 tiles), half tiles only (48 tiles); K below one 128-deep k-step; integer
+    operands, so the output must equal the oracle bit for bit, with guard sentinels around it."""
+    from h3_tp2_amd import ops
+    a, w, sa, sb = int_operands(M, N, K, seed=7 * M + N + K, device=cuda)
+    ref = ref_gemm(a, w, sa, sb)
+    guard = 4096
+    buf = torch.full((M * N + 2 * guard,), float("nan"), device=cuda, dtype=torch.bfloat16)
+    buf[:guard] = 7.0
+    buf[-guard:] = 7.0
+    y = buf[guard:guard + M * N].view(M, N)
+    ops.gemm(a, w, sa, sb, torch.bfloat16, out=y)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(y), ref)
+    assert bool((buf[:guard] == 7.0).all()) and bool((buf[-guard:] == 7.0).all())
