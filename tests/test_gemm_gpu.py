@@ -91,10 +91,12 @@ def test_measured_shapes_within_tolerance(cuda, name):
     check_close_bf16(y, ref_gemm_exact(a, w, sa, sb), gemm_acc_err(a, w, sa, sb))
 
 
-def test_fused_row_amax_and_quant(cuda):
+@pytest.mark.parametrize("M,N,K", [(777, 3072, 1024), (4100, 4368, 256), (2300, 3600, 256)])
+def test_fused_row_amax_and_quant(cuda, M, N, K):
+    """The fused next-layer quant: the row maxima and the quant from them equal the plain GEMM's output and kernel 1 on
+    it, for half tiles only (48 tiles), whole rounds plus a half-tile tail (306) and full tiles only (135)."""
     from h3_tp2_amd import ops
-    M, N, K = 777, 3072, 1024
-    a, w, sa, sb = serving_like(M, N, K, seed=3, device=cuda)
+    a, w, sa, sb = serving_like(M, N, K, seed=3 + M, device=cuda)
     amax = torch.full((M,), 123.0, device=cuda)          # the library zeroes it first
     y = ops.gemm(a, w, sa, sb, torch.bfloat16, row_amax=amax)
     torch.cuda.synchronize()
