@@ -1,25 +1,28 @@
 """Benchmark of the online-FP8 DiT linear path on one MI355X: prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only WORKLOAD]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--preroll-s S] [--no-cpu] [--only WORKLOADS]
 
-Headline workload (``value``): the QKV projection at the 5 s 960x576 token count -- X bf16 [16740, 3072] quantised
-per token to e4m3fn (kernel 1), then the scaled FP8 GEMM against the per-channel-quantised QKV weight [9216, 3072]
-with a bf16 output (kernel 2).  A step is one quant + one GEMM over the whole token sequence, inputs resident in HBM;
-``value`` = 2 M N K / (step time) in TFLOP/s.  ``roofline`` is the GEMM kernel alone against the FP8 dense MFMA peak
-(5.0 PFLOP/s), its average launch time measured with HIP events on the launch stream.  The other measured workloads
-(the single linear, the fused FFN and the 15 s block chain at 1344x768, the grouped launch, the quant / SwiGLU-tail
-passes and the producers with the quant fused in, against the 8 TB/s HBM peak) are reported under ``workloads``.
-``cpu_baseline`` times the CPU oracle of the reference's torch CPU path (per-token quant, fp32 product, scaled
-epilogue) on the headline workload's full token count on this host's cores, repeated for about 10 s (median run).
-The default 100 untimed warm-up steps let the chip's clock settle: over the first few tens of heavy calls the GEMM's
-launch time swings between about 345 and 460 us before it steadies.  Synthetic seeded inputs, random-init weights (no
-checkpoints).
+Headline workload (``value``): the full DiT block linear chain at the 15 s 1344x768 token count (M = 91 728 tokens,
+hidden 3072), the set the target is quoted on.  One step is: X -> per-token quant (kernel 1) -> QKV GEMM [3072 -> 9216]
+(kernel 2); the attention-output stand-in -> quant -> out-projection [3072 -> 3072] whose epilogue reduces the row
+maxima, and the quant tail from them; gate/up GEMM [3072 -> 2 x 8192] with the SwiGLU epilogue (kernel 3) and its
+requant tail; down GEMM [8192 -> 3072] with the next block's quant fused the same way.  ``value`` = the chain's
+2 M (3 H^2 + H^2 + 2 F H + F H) FLOPs / step time, in TFLOP/s, inputs resident in HBM.  Every kernel launch of the
+timed steps is bracketed by HIP events on the launch stream, so the per-kernel averages (``breakdown``) and
+``roofline`` come from the same timed region: ``roofline`` is kernel 3 (gate/up + SwiGLU, 44 % of the chain's FLOPs)
+against the 5.0 PFLOP/s FP8 dense MFMA peak.  Before the warm-up steps an explicit pre-roll runs the chain for
+``--preroll-s`` seconds: the chip's clock moves over the first heavy calls, and the pre-roll makes the timed steps
+independent of how short the warm-up is.  The other measured workloads (the QKV projection at 960x576, the single
+linear, the FFN at 1344x768 5 s, the grouped launch, the producers / consumers passes, the vendor GEMM) are reported
+under ``workloads``.  ``cpu_baseline`` times the reference's torch CPU path (oracle/torch_path.py) of the same chain on
+a row sample, on this host's cores.  Synthetic seeded inputs, random-init weights (no checkpoints).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -34,16 +37,50 @@ PEAK_GBS = 8000.0             # MI355X HBM3E
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=100,
-                    help="untimed steps first (the chip's clock settles over the first few tens of heavy calls)")
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--preroll-s", type=float, default=1.0,
+                    help="seconds of untimed chain steps before the warm-up (lets the chip's clock settle)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
-    ap.add_argument("--cpu-rows", type=int, default=0, help="token rows of the CPU baseline sample (0: all)")
+    ap.add_argument("--only", default="", help="comma list of the extra workloads to run (default: all; 'none': none)")
+    ap.add_argument("--cpu-rows", type=int, default=2048, help="token rows of the CPU baseline sample")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU baseline for at least this long")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 512 MiB device-to-device copy (the known-size kernel that scales PMC byte counts)")
     return ap.parse_args()
+
+
+def host_cpu() -> dict:
+    """CPU model, physical cores and the threads this process may use (lscpu, else /proc/cpuinfo)."""
+    info = {"model": None, "physical_cores": None}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {ln.split(":", 1)[0].strip(): ln.split(":", 1)[1].strip() for ln in out.splitlines() if ":" in ln}
+        info["model"] = kv.get("Model name")
+        if kv.get("Core(s) per socket") and kv.get("Socket(s)"):
+            info["physical_cores"] = int(kv["Core(s) per socket"]) * int(kv["Socket(s)"])
+    except (OSError, subprocess.SubprocessError, ValueError):
+        pass
+    if info["model"] is None and os.path.exists("/proc/cpuinfo"):
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                info["model"] = ln.split(":", 1)[1].strip()
+                break
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS")
+    info["threads"] = min(avail, int(env)) if env and env.isdigit() and int(env) > 0 else avail
+    info["logical_cpus_visible"] = avail
+    return info
+
+
+def profile_traffic(name: str):
+    """Bytes per launch from a committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
+    path = os.path.join(ROOT, "profiles", name)
+    if os.path.exists(path):
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1]), f"profiles/{name} (rocprofv3 --pmc, not measured in this run)"
+    return None, None
 
 
 def main() -> None:
@@ -83,6 +120,12 @@ def main() -> None:
         w, sw = ops.quant_rows(synthetic.weight(N, K, seed).to(dev))
         return w, sw.view(-1)
 
+    def tflops(f, ms):
+        return f / (ms * 1e-3) / 1e12
+
+    def gbs(b, ms):
+        return b / (ms * 1e-3) / 1e9
+
     out = {}
 
     if args.copy_calibration:
@@ -93,62 +136,176 @@ def main() -> None:
         torch.cuda.synchronize()
         del src, dst
 
-    # ---- headline: QKV projection, 960x576 5 s (M = 31 x 540) ----
-    c2 = synthetic.CONFIGS["c2_qkv_960x576_5s"]
-    M, K, N = c2["M"], c2["K"], c2["N"]
-    x = synthetic.activations(M, K, seed=0, n_out=c2["n_out"]).to(dev)
-    w, sw = quantised_weight(N, K, seed=1)
-    q = torch.empty((M, K), device=dev, dtype=ops.E4M3)
-    sq = torch.empty((M, 1), device=dev, dtype=torch.float32)
-    y = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    # ---- headline: the block linear chain at 1344x768 15 s (M = 91 x 1008) ----
+    c4 = synthetic.CONFIGS["c4_chain_1344x768_15s"]
+    M, H, F = c4["M"], c4["K"], 8192
+    x4 = synthetic.activations(M, H, seed=0, n_out=c4["n_out"]).to(dev)
+    xo = synthetic.activations(M, H, seed=5, n_out=c4["n_out"]).to(dev)     # attention-output stand-in
+    wqkv, sqkv = quantised_weight(3 * H, H, seed=1)
+    wo, so = quantised_weight(H, H, seed=4)
+    wgu, sgu = quantised_weight(2 * F, H, seed=2)
+    wd, sd = quantised_weight(H, F, seed=3)
+    E4 = ops.E4M3
 
-    def qkv_step():
-        ops.quant_rows(x, q, sq)
-        ops.gemm(q, w, sq, sw, torch.bfloat16, out=y)
+    def buf(shape, dt):
+        return torch.empty(shape, device=dev, dtype=dt)
 
+    q0, s0 = buf((M, H), E4), buf((M, 1), torch.float32)
+    yqkv = buf((M, 3 * H), torch.bfloat16)
+    qo, s_o = buf((M, H), E4), buf((M, 1), torch.float32)
+    y_out, amax_o = buf((M, H), torch.bfloat16), buf((M,), torch.float32)
+    qg, sg = buf((M, H), E4), buf((M, 1), torch.float32)
+    hws, amax_h = buf((M, F), torch.bfloat16), buf((M,), torch.float32)
+    qh, sh = buf((M, F), E4), buf((M, 1), torch.float32)
+    y_d, amax_d = buf((M, H), torch.bfloat16), buf((M,), torch.float32)
+    qn, sn = buf((M, H), E4), buf((M, 1), torch.float32)
+
+    # (name, launch, algorithmic FLOPs, algorithmic HBM bytes) of every kernel launch of one chain step, in order
+    seg = [
+        ("quant_x [M,3072] (kernel 1)", lambda: ops.quant_rows(x4, q0, s0), 0.0, 3.0 * M * H + 4 * M),
+        ("qkv_gemm 3072->9216 (kernel 2)", lambda: ops.gemm(q0, wqkv, s0, sqkv, torch.bfloat16, out=yqkv),
+         2.0 * M * 3 * H * H, 0.0),
+        ("quant_attn [M,3072] (kernel 1)", lambda: ops.quant_rows(xo, qo, s_o), 0.0, 3.0 * M * H + 4 * M),
+        ("out_gemm 3072->3072 + row amax (kernel 2)",
+         lambda: ops.gemm(qo, wo, s_o, so, torch.bfloat16, out=y_out, row_amax=amax_o), 2.0 * M * H * H, 0.0),
+        ("out quant tail [M,3072]", lambda: ops.quant_rows_amax(y_out, amax_o, qg, sg), 0.0, 3.0 * M * H + 4 * M),
+        ("gate_up_swiglu 3072->2x8192 + row amax (kernel 3)",
+         lambda: ops.gemm_swiglu(qg, wgu, sg, sgu, row_amax=amax_h, out=hws), 2.0 * M * 2 * F * H, 0.0),
+        ("swiglu requant tail [M,8192]", lambda: ops.quant_rows_amax(hws, amax_h, qh, sh), 0.0, 3.0 * M * F + 4 * M),
+        ("down_gemm 8192->3072 + row amax (kernel 2)",
+         lambda: ops.gemm(qh, wd, sh, sd, torch.bfloat16, out=y_d, row_amax=amax_d), 2.0 * M * H * F, 0.0),
+        ("down quant tail [M,3072]", lambda: ops.quant_rows_amax(y_d, amax_d, qn, sn), 0.0, 3.0 * M * H + 4 * M),
+    ]
+    IDX_K3 = 5                                               # kernel 3's launch in `seg`
+    flops = sum(x[2] for x in seg)
+
+    def chain_step(marks=None):
+        for i, (_, fn, _, _) in enumerate(seg):
+            if marks is not None:
+                marks[i].record(stream)
+            fn()
+        if marks is not None:
+            marks[len(seg)].record(stream)
+
+    # clock pre-roll, then the warm-up steps, then the timed steps with one event before every launch
+    t_pre = time.perf_counter()
+    n_pre = 0
+    while time.perf_counter() - t_pre < args.preroll_s or n_pre < 2:
+        chain_step()
+        n_pre += 1
+        if n_pre % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    preroll_ms = (time.perf_counter() - t_pre) * 1e3
     steps, warm = args.steps, args.warmup
-    t_step = time_steps(qkv_step, steps, warm) / steps
-    flops = 2.0 * M * N * K
-    t_gemm = time_steps(lambda: ops.gemm(q, w, sq, sw, torch.bfloat16, out=y), steps, warm) / steps
-    t_quant = time_steps(lambda: ops.quant_rows(x, q, sq), steps, warm) / steps
-    value = flops / (t_step * 1e-3) / 1e12
-    gemm_tf = flops / (t_gemm * 1e-3) / 1e12
-    quant_bytes = 3.0 * M * K + 4.0 * M
-    out["qkv_quant"] = {"ms": round(t_quant, 4), "GB/s": round(quant_bytes / (t_quant * 1e-3) / 1e9, 1),
-                        "frac_hbm": round(quant_bytes / (t_quant * 1e-3) / 1e9 / PEAK_GBS, 4)}
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "gemm_qkv_960x576_traffic.txt")
-    if os.path.exists(tpath):
-        for line in open(tpath):
-            if line.startswith("traffic_bytes_per_launch:"):
-                traffic = float(line.split(":", 1)[1])
-
-    roofline = {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(gemm_tf / PEAK_TFLOPS, 4), "traffic": traffic,
-                "kernel": "gemm_kernel<bf16> (kernel 2: full-tile rounds + half-tile tail)", "launch_ms": round(t_gemm, 4),
-                "flops_per_launch": flops}
-    del x
+    for _ in range(warm):
+        chain_step()
+    marks = [[ev() for _ in range(len(seg) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0, t1 = ev(), ev()
+    t0.record(stream)
+    for k in range(steps):
+        chain_step(marks[k])
+    t1.record(stream)
+    t1.synchronize()
+    torch.cuda.synchronize()
+    t_step = t0.elapsed_time(t1) / steps
+    value = tflops(flops, t_step)
+    seg_ms = [sum(marks[k][i].elapsed_time(marks[k][i + 1]) for k in range(steps)) / steps for i in range(len(seg))]
+    breakdown = {}
+    for (name, _, f, b), ms in zip(seg, seg_ms):
+        e = {"ms": round(ms, 4)}
+        if f:
+            e["TFLOP/s"] = round(tflops(f, ms), 1)
+            e["frac_mfma"] = round(tflops(f, ms) / PEAK_TFLOPS, 4)
+        else:
+            e["GB/s"] = round(gbs(b, ms), 1)
+            e["frac_hbm"] = round(gbs(b, ms) / PEAK_GBS, 4)
+        breakdown[name] = e
+    gemm_ms = sum(ms for (_, _, f, _), ms in zip(seg, seg_ms) if f)
+    k3_tf = tflops(seg[IDX_K3][2], seg_ms[IDX_K3])
+    traffic, traffic_src = profile_traffic("gemm_swiglu_c4_1344x768_15s_traffic.txt")
+    roofline = {"bound": "mfma", "achieved": round(k3_tf, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(k3_tf / PEAK_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "kernel": "gemm_kernel<EPI_SWIGLU> (kernel 3: gate/up GEMM + SwiGLU epilogue + row amax), c4",
+                "launch_ms": round(seg_ms[IDX_K3], 4), "flops_per_launch": seg[IDX_K3][2],
+                "timing": f"HIP events around each of the {steps} timed launches on the launch stream (the row-amax "
+                          "zero-fill kernel before it included)"}
+    c4_line = {"breakdown": breakdown,
+               "gemms_TFLOP/s": round(tflops(flops, gemm_ms), 1),
+               "gemms_frac_mfma": round(tflops(flops, gemm_ms) / PEAK_TFLOPS, 4),
+               "sum_of_launches_ms": round(sum(seg_ms), 4),
+               "step_minus_launches_ms": round(t_step - sum(seg_ms), 4),
+               "note": "out-proj input is a seeded bf16 stand-in for the attention output; value counts the four "
+                       "GEMMs' FLOPs over the whole step (quant and tail passes included in the time)"}
+    del x4, xo, yqkv, hws, y_out, y_d, q0, qo, qg, qh, qn
 
     # ---- the other measured workloads ----
     def want(name):
-        return not only or name in only
+        return "none" not in only and (not only or name in only)
 
-    if want("vendor"):
-        # The same GEMM through the vendor library (torch._scaled_mm -> hipBLASLt) on the same fp8 operands and
-        # per-token / per-channel scales, bf16 out: the practical reference point for kernel 2 on this chip.
-        try:
-            sa2, sb2 = sq.view(M, 1), sw.view(1, N)
-            t_v = time_steps(lambda: torch._scaled_mm(q, w.t(), sa2, sb2, out_dtype=torch.bfloat16), steps, warm) / steps
-            one = torch.ones((), device=dev)
-            t_vt = time_steps(lambda: torch._scaled_mm(q, w.t(), one, one, out_dtype=torch.bfloat16), steps, warm) / steps
-            out["vendor_gemm_qkv_960x576"] = {
-                "library": "torch._scaled_mm (hipBLASLt)",
-                "rowwise_scales_TFLOP/s": round(flops / (t_v * 1e-3) / 1e12, 1),
-                "tensorwise_scales_TFLOP/s": round(flops / (t_vt * 1e-3) / 1e12, 1),
-                "kernel2_TFLOP/s": round(gemm_tf, 1)}
-        except Exception as exc:  # noqa: BLE001
-            out["vendor_gemm_qkv_960x576"] = {"error": f"{type(exc).__name__}: {str(exc)[:160]}"}
+    if want("c2") or want("vendor"):
+        # The QKV projection at the 5 s 960x576 token count (M = 31 x 540): quant of X + kernel 2, with the two
+        # launches timed by events inside the timed steps (the gap between the step and its launches is what the
+        # host's back-to-back launches leave between them).
+        c2 = synthetic.CONFIGS["c2_qkv_960x576_5s"]
+        M2, K2, N2 = c2["M"], c2["K"], c2["N"]
+        x2 = synthetic.activations(M2, K2, seed=0, n_out=c2["n_out"]).to(dev)
+        w2, sw2 = quantised_weight(N2, K2, seed=1)
+        q2, sq2 = buf((M2, K2), E4), buf((M2, 1), torch.float32)
+        y2 = buf((M2, N2), torch.bfloat16)
+        f2 = 2.0 * M2 * N2 * K2
+        ev2 = [[ev() for _ in range(3)] for _ in range(steps)]
+
+        def c2_step(m=None):
+            if m:
+                m[0].record(stream)
+            ops.quant_rows(x2, q2, sq2)
+            if m:
+                m[1].record(stream)
+            ops.gemm(q2, w2, sq2, sw2, torch.bfloat16, out=y2)
+            if m:
+                m[2].record(stream)
+        for _ in range(max(warm, 20)):
+            c2_step()
+        torch.cuda.synchronize()
+        a0, a1 = ev(), ev()
+        a0.record(stream)
+        for k in range(steps):
+            c2_step(ev2[k])
+        a1.record(stream)
+        a1.synchronize()
+        t2 = a0.elapsed_time(a1) / steps
+        tq2 = sum(e[0].elapsed_time(e[1]) for e in ev2) / steps
+        tg2 = sum(e[1].elapsed_time(e[2]) for e in ev2) / steps
+        qb2 = 3.0 * M2 * K2 + 4.0 * M2
+        if want("c2"):
+            out["c2_qkv_960x576_5s"] = {
+                "ms_per_step": round(t2, 4), "TFLOP/s": round(tflops(f2, t2), 1),
+                "kernel2_ms": round(tg2, 4), "kernel2_TFLOP/s": round(tflops(f2, tg2), 1),
+                "kernel2_frac_mfma": round(tflops(f2, tg2) / PEAK_TFLOPS, 4),
+                "quant_ms": round(tq2, 4), "quant_GB/s": round(gbs(qb2, tq2), 1),
+                "quant_frac_hbm": round(gbs(qb2, tq2) / PEAK_GBS, 4),
+                "step_minus_launches_ms": round(t2 - tq2 - tg2, 4)}
+        if want("vendor"):
+            # The same GEMM through the vendor library (torch._scaled_mm -> hipBLASLt) on the same fp8 operands and
+            # per-token / per-channel scales, bf16 out: the practical reference point for kernel 2 on this chip.
+            try:
+                sa2, sb2 = sq2.view(M2, 1), sw2.view(1, N2)
+                t_v = time_steps(lambda: torch._scaled_mm(q2, w2.t(), sa2, sb2, out_dtype=torch.bfloat16), steps,
+                                 warm) / steps
+                one = torch.ones((), device=dev)
+                t_vt = time_steps(lambda: torch._scaled_mm(q2, w2.t(), one, one, out_dtype=torch.bfloat16), steps,
+                                  warm) / steps
+                t_k2 = time_steps(lambda: ops.gemm(q2, w2, sq2, sw2, torch.bfloat16, out=y2), steps, warm) / steps
+                out["vendor_gemm_qkv_960x576"] = {
+                    "library": "torch._scaled_mm (hipBLASLt)",
+                    "rowwise_scales_TFLOP/s": round(tflops(f2, t_v), 1),
+                    "tensorwise_scales_TFLOP/s": round(tflops(f2, t_vt), 1),
+                    "kernel2_TFLOP/s": round(tflops(f2, t_k2), 1)}
+            except Exception as exc:  # noqa: BLE001
+                out["vendor_gemm_qkv_960x576"] = {"error": f"{type(exc).__name__}: {str(exc)[:160]}"}
+        del x2, w2, q2, y2
 
     if want("c1"):
         c = synthetic.CONFIGS["c1_single_linear"]
@@ -206,38 +363,6 @@ def main() -> None:
                                           "frac_hbm": round(sq_bytes / (t_sq * 1e-3) / 1e9 / PEAK_GBS, 4)}}
         del x3, wgu, wd, q3, hws, y3, h_in, gu_in, hq
 
-    if want("c4"):
-        c = synthetic.CONFIGS["c4_chain_1344x768_15s"]
-        M4, K4 = c["M"], c["K"]
-        F4 = 8192
-        x4 = synthetic.activations(M4, K4, seed=0, n_out=c["n_out"]).to(dev)
-        xo = synthetic.activations(M4, K4, seed=5, n_out=c["n_out"]).to(dev)   # attention output stand-in
-        wqkv, sqkv = quantised_weight(3 * K4, K4, seed=1)
-        wo, so = quantised_weight(K4, K4, seed=4)
-        wgu, sgu = quantised_weight(2 * F4, K4, seed=2)
-        wd, sd = quantised_weight(K4, F4, seed=3)
-        q4 = torch.empty((M4, K4), device=dev, dtype=ops.E4M3)
-        s4 = torch.empty((M4, 1), device=dev, dtype=torch.float32)
-        yqkv = torch.empty((M4, 3 * K4), device=dev, dtype=torch.bfloat16)
-        hws = torch.empty((M4, F4), device=dev, dtype=torch.bfloat16)
-
-        def c4_step():
-            ops.quant_rows(x4, q4, s4)                                       # block input -> fp8
-            ops.gemm(q4, wqkv, s4, sqkv, torch.bfloat16, out=yqkv)           # QKV (to attention)
-            qo, so_ = ops.quant_rows(xo)                                     # attention output -> fp8
-            _, qg, sg = ops.gemm_quant(qo, wo, so_, so)                      # out-proj + fused quant
-            qh, sh = ops.gemm_swiglu_quant(qg, wgu, sg, sgu, h_ws=hws)       # gate/up + SwiGLU + requant
-            ops.gemm_quant(qh, wd, sh, sd)                                   # down + next block's quant
-        t = time_steps(c4_step, max(2, steps // 4), max(1, warm // 2)) / max(2, steps // 4)
-        f4 = 2.0 * M4 * (3 * K4 * K4 + K4 * K4 + 2 * F4 * K4 + K4 * F4)
-        t_q = time_steps(lambda: ops.quant_rows(x4, q4, s4), steps, warm) / steps
-        qb = 3.0 * M4 * K4 + 4.0 * M4
-        out["c4_chain_1344x768_15s"] = {"ms": round(t, 3), "TFLOP/s": round(f4 / (t * 1e-3) / 1e12, 1),
-                                        "quant_3072": {"GB/s": round(qb / (t_q * 1e-3) / 1e9, 1),
-                                                       "frac_hbm": round(qb / (t_q * 1e-3) / 1e9 / PEAK_GBS, 4)},
-                                        "note": "out-proj input is a seeded bf16 stand-in for the attention output"}
-        del x4, xo, wqkv, wo, wgu, wd, q4, yqkv, hws
-
     if want("c5"):
         groups = synthetic.CONFIGS["c5_grouped"]["groups"]
         probs, xs = [], []
@@ -265,10 +390,11 @@ def main() -> None:
     if want("producers"):
         # The quant fused into its producers: norm1 + AdaLN -> QKV input at the 960x576 5 s token count, the gated
         # residual + norm2 + AdaLN -> fc1 input at the 1344x768 5 s count; H = 3072, a [6, 6H] modulation table.
-        H = K
+        H = 3072
+        M_qkv = synthetic.CONFIGS["c2_qkv_960x576_5s"]["M"]
         gen = torch.Generator(device=dev).manual_seed(7)
         res = {}
-        for name, Mp, gate in (("qkv_rms_quant_16740x3072", M, False), ("fc1_gate_rms_quant_31248x3072",
+        for name, Mp, gate in (("qkv_rms_quant_16740x3072", M_qkv, False), ("fc1_gate_rms_quant_31248x3072",
                                                                          synthetic.CONFIGS["c3_ffn_1344x768_5s"]["M"],
                                                                          True)):
             xp = (torch.randn(Mp, H, device=dev, generator=gen)
@@ -308,7 +434,7 @@ def main() -> None:
         from h3_tp2_amd import fp8_consumers as fc
         gen = torch.Generator(device=dev).manual_seed(9)
         res = {}
-        T, Hq = M, K // 128
+        T, Hq, N = synthetic.CONFIGS["c2_qkv_960x576_5s"]["M"], 3072 // 128, 9216
         x32 = torch.randn(T, N, device=dev, generator=gen) * 3000
         sa_t = torch.rand(T, device=dev, generator=gen) * 1e-3 + 1e-4
         sb_t = torch.rand(N, device=dev, generator=gen) * 1e-3 + 1e-4
@@ -321,7 +447,7 @@ def main() -> None:
         res["qkv_qk_norm_rope_16740x9216"] = {"ms": round(t_qk, 4), "GB/s": round(qk_bytes / (t_qk * 1e-3) / 1e9, 1),
                                               "frac_hbm": round(qk_bytes / (t_qk * 1e-3) / 1e9 / PEAK_GBS, 4)}
         del x32, st
-        Mc, H = synthetic.CONFIGS["c3_ffn_1344x768_5s"]["M"], K
+        Mc, H = synthetic.CONFIGS["c3_ffn_1344x768_5s"]["M"], 3072
         x32 = torch.randn(Mc, H, device=dev, generator=gen) * 3000
         sa_c = torch.rand(Mc, device=dev, generator=gen) * 1e-3 + 1e-4
         sb_c = torch.rand(H, device=dev, generator=gen) * 1e-3 + 1e-4
@@ -343,40 +469,47 @@ def main() -> None:
         del x32, st, resid, ada
         out["consumers_of_fp32_product"] = res
 
-    # ---- CPU baseline: the oracle of the reference's torch CPU path on the headline workload ----
+    # ---- CPU baseline: the reference's torch CPU path of the headline chain on a row sample ----
     cpu = None
     if not args.no_cpu:
         sys.path.insert(0, ROOT)
-        import numpy as np
-
-        from oracle import oracle as O
-        rows = min(args.cpu_rows, M) if args.cpu_rows > 0 else M
-        xs = synthetic.activations(M, K, seed=0, n_out=c2["n_out"])[:rows]
-        xb = xs.view(torch.int16).numpy().view(np.uint16)
-        wb = synthetic.weight(N, K, seed=1).view(torch.int16).numpy().view(np.uint16)
-        wq, swq = O.quant_rows(wb)
-        O.linear(xb[:16], wq, swq)                                           # warm-up
+        from oracle import torch_path as TP
+        hc = host_cpu()
+        torch.set_num_threads(hc["threads"])
+        rows = max(1, min(args.cpu_rows, M))
+        xc = synthetic.activations(M, H, seed=0, n_out=c4["n_out"])[:rows]
+        xoc = synthetic.activations(M, H, seed=5, n_out=c4["n_out"])[:rows]
+        wts = {}
+        for key, (n, k, seed) in {"qkv": (3 * H, H, 1), "out": (H, H, 4), "gate_up": (2 * F, H, 2),
+                                  "down": (H, F, 3)}.items():
+            wq_, sw_ = TP.quant(synthetic.weight(n, k, seed))
+            wts[key] = (wq_, sw_.view(-1))
+        TP.chain_step(xc[:64], xoc[:64], wts)                               # warm-up
         runs = []
         while len(runs) < 3 or sum(runs) < args.cpu_seconds:
-            t0 = time.perf_counter()
-            O.linear(xb, wq, swq)
-            runs.append(time.perf_counter() - t0)
-        med = sorted(runs)[len(runs) // 2]
-        t_full = med * M / rows
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        cpu = {"value": round(flops / t_full / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-               "sample": f"oracle per-token quant + numpy fp32 product + C epilogue on {rows} of {M} token rows, "
-                         f"median of {len(runs)} runs ({med:.2f} s each, {sum(runs):.1f} s in all)"
-                         + ("" if rows == M else f", scaled linearly to {M} rows"),
-               "host_cpu_count": os.cpu_count()}
+            t_a = time.perf_counter()
+            TP.chain_step(xc, xoc, wts)
+            runs.append(time.perf_counter() - t_a)
+        best = min(runs)
+        f_rows = flops * rows / M
+        cpu = {"value": round(f_rows / best / 1e12, 5), "unit": "TFLOP/s", "cores": hc["threads"], "kind": "port",
+               "sample": f"the block chain (quant, fp32 torch matmul, epilogue; SwiGLU + requant) through the reference's "
+                         f"torch CPU mirrors (oracle/torch_path.py) on the first {rows} of {M} token rows; min of "
+                         f"{len(runs)} runs ({best:.2f} s; {sum(runs):.1f} s in all); the rate holds per row, so the "
+                         f"full chain would take {best * M / rows:.1f} s",
+               "cpu_model": hc["model"], "physical_cores": hc["physical_cores"],
+               "logical_cpus_visible": hc["logical_cpus_visible"], "torch_threads": torch.get_num_threads()}
 
     line = {"metric": METRIC, "value": round(value, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
             "warmup": warm, "ms_per_step": round(t_step, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "e4m3", "data": "synthetic (seeded N(0,1) activations with x40 outlier "
             "channels, random-init N(0,0.02) weights)",
-            "config": {"workload": "qkv_960x576_5s: quant X[16740,3072] + FP8 GEMM vs W[9216,3072], bf16 out",
-                       "M": M, "K": K, "N": N, "parallelism": "single GPU"},
-            "roofline": roofline, "cpu_baseline": cpu, "workloads": out}
+            "config": {"workload": "c4_chain_1344x768_15s: DiT block linear set QKV 3072->9216, out 3072->3072, "
+                                   "gate/up 3072->2x8192 + SwiGLU, down 8192->3072, each input quantised per token "
+                                   "(the next one fused into the previous epilogue)",
+                       "M": M, "hidden": H, "ffn": F, "parallelism": "single GPU"},
+            "preroll": {"ms": round(preroll_ms, 1), "chain_steps": n_pre},
+            "roofline": roofline, "chain": c4_line, "cpu_baseline": cpu, "workloads": out}
     print(json.dumps(line))
 
 

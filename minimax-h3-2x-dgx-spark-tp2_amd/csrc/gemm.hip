@@ -497,6 +497,14 @@ __device__ __forceinline__ uint32_t max_abs_bf16x2(uint32_t m, uint32_t p) {
     return m > hi ? m : hi;
 }
 
+// The same for a packed fp16 pair: each half is widened to fp32 (exact) before its |.| bits are compared, so the row
+// maximum is the fp32 value of the largest rounded fp16 output (NaN patterns exceed every finite one, as above).
+__device__ __forceinline__ uint32_t max_abs_f16x2(uint32_t m, uint32_t p) {
+    const uint32_t lo = f2u(fp16_to_f32(p & 0xffffu)) & 0x7fffffffu, hi = f2u(fp16_to_f32(p >> 16)) & 0x7fffffffu;
+    m = m > lo ? m : lo;
+    return m > hi ? m : hi;
+}
+
 // x + 0: -0 becomes +0 (round to nearest), every other value (NaN included) is unchanged.
 __device__ __forceinline__ float zero_to_pos(float x) {
     float z = 0.0f;
@@ -689,7 +697,9 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                             lo = cvt_bf16x2(v[0], v[1]);
                             hi2 = cvt_bf16x2(v[2], v[3]);
                         }
-                        if (EPI == EPI_AMAX && ok) rmax = max_abs_bf16x2(max_abs_bf16x2(rmax, lo), hi2);
+                        if (EPI == EPI_AMAX && ok)
+                            rmax = OUT_DT ? max_abs_f16x2(max_abs_f16x2(rmax, lo), hi2)
+                                          : max_abs_bf16x2(max_abs_bf16x2(rmax, lo), hi2);
                         put4(mj, cl, lo, hi2);
                     }
                 }
@@ -878,11 +888,12 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
              int64_t sa_stride, const float* sb, int64_t sb_stride, const void* bias, void* y, int64_t ldy,
              int out_dt, int64_t M, int64_t N, int64_t K, int64_t w_rows, float* row_amax, const uint16_t* silu,
              hipStream_t st) {
+    const int out_elem = (out_dt == H3FP8_DT_F32) ? 4 : 2;
     int64_t rows_per = std::max<int64_t>(BM, ((kMaxBufferBytes - K) / lda + 1) / BM * BM);
     if (sa_stride > 0) rows_per = std::min<int64_t>(rows_per, std::max<int64_t>(BM, kMaxBufferBytes / (4 * sa_stride) / BM * BM));
-    // the output's byte offsets (stored through a range-checked descriptor) are 32-bit as well
-    rows_per = std::min<int64_t>(rows_per, std::max<int64_t>(BM, kMaxBufferBytes / (4 * ldy) / BM * BM));
-    const int out_elem = (out_dt == H3FP8_DT_F32) ? 4 : 2;
+    // the output's byte offsets (stored through a range-checked descriptor) are 32-bit as well: rows of ldy elements of
+    // out_elem bytes (a bf16 [91 728, 9216] output fits one launch)
+    rows_per = std::min<int64_t>(rows_per, std::max<int64_t>(BM, kMaxBufferBytes / (out_elem * ldy) / BM * BM));
     for (int64_t r0 = 0; r0 < M; r0 += rows_per) {
         const int64_t Mi = std::min<int64_t>(rows_per, M - r0);
         GroupedParams gp{};

@@ -39,6 +39,33 @@ def _rows(t: torch.Tensor, name: str) -> int:
     return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], t.stride(0))
 
 
+def check_buffer(t: torch.Tensor, name: str, shape: tuple, dtype: torch.dtype, device: torch.device,
+                 contiguous: bool = False) -> None:
+    """A caller-supplied output or workspace must be exactly what the kernel will write: the shape, dtype and device
+    given, rows contiguous (or the whole tensor, with ``contiguous``).  A wrong buffer raises here, before any launch,
+    instead of becoming an out-of-bounds device write."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor, got {type(t).__name__}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.dim() == 2:
+        _rows(t, name)
+
+
+def _scale_out(t: torch.Tensor, name: str, M: int, device: torch.device) -> None:
+    """A per-token scale output: M fp32 entries, contiguous, viewed as [M, 1] or [M]."""
+    shape = tuple(t.shape) if isinstance(t, torch.Tensor) else None
+    if shape not in ((M, 1), (M,)):
+        raise ValueError(f"{name} must have shape ({M}, 1) or ({M},), got {shape}")
+    check_buffer(t, name, shape, torch.float32, device, contiguous=True)
+
+
 def scale_vec(scale: torch.Tensor, n: int, name: str) -> tuple[torch.Tensor, int]:
     """(fp32 tensor, element stride) for a per-row/per-column scale of n entries, or a scalar (stride 0)."""
     if scale.dtype != torch.float32:
@@ -69,8 +96,10 @@ def quant_rows(x: torch.Tensor, q: torch.Tensor | None = None, scale: torch.Tens
     ldx = _rows(x, "x")
     if q is None:
         q = torch.empty((M, K), device=x.device, dtype=E4M3)
+    check_buffer(q, "q", (M, K), E4M3, x.device)
     if scale is None:
         scale = torch.empty((M, 1), device=x.device, dtype=torch.float32)
+    _scale_out(scale, "scale", M, x.device)
     _lib.call("h3fp8_quant_rows", x.data_ptr(), ldx, M, K, q.data_ptr(), _rows(q, "q"), scale.data_ptr(), _stream(x))
     return q, scale
 
@@ -79,11 +108,16 @@ def quant_rows_amax(x: torch.Tensor, row_amax: torch.Tensor, q: torch.Tensor | N
                     scale: torch.Tensor | None = None):
     """Per-token quant of bf16 [M, K] with the row maxima given (the tail pass of a fused-amax GEMM)."""
     _need_cuda(x, row_amax)
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise ValueError(f"quant_rows_amax takes bf16 [M, K], got {x.dtype} {tuple(x.shape)}")
     M, K = x.shape
+    check_buffer(row_amax, "row_amax", (M,), torch.float32, x.device, contiguous=True)
     if q is None:
         q = torch.empty((M, K), device=x.device, dtype=E4M3)
+    check_buffer(q, "q", (M, K), E4M3, x.device)
     if scale is None:
         scale = torch.empty((M, 1), device=x.device, dtype=torch.float32)
+    _scale_out(scale, "scale", M, x.device)
     _lib.call("h3fp8_quant_rows_amax", x.data_ptr(), _rows(x, "x"), M, K, row_amax.data_ptr(), q.data_ptr(),
               _rows(q, "q"), scale.data_ptr(), _stream(x))
     return q, scale
@@ -142,9 +176,13 @@ def gemm(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch
     M, sa, sa_st, sb, sb_st = _gemm_args(a, w, scale_a, scale_b, N)
     if out_dtype not in _DT:
         raise ValueError(f"out_dtype must be bf16, fp16 or fp32 (probe), got {out_dtype}")
-    if bias is not None and (bias.dim() != 1 or bias.numel() != N or bias.dtype != out_dtype):
-        raise ValueError("bias must be [N] in the output dtype")
+    if bias is not None and (bias.dim() != 1 or bias.numel() != N or bias.dtype != out_dtype
+                             or bias.device != a.device or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous [N] vector in the output dtype on the operands' device")
     y = out if out is not None else torch.empty((M, N), device=a.device, dtype=out_dtype)
+    check_buffer(y, "out", (M, N), out_dtype, a.device)
+    if row_amax is not None:
+        check_buffer(row_amax, "row_amax", (M,), torch.float32, a.device, contiguous=True)
     _lib.call("h3fp8_gemm", a.data_ptr(), _rows(a, "a"), w.data_ptr(), _rows(w, "w"), sa.data_ptr(), sa_st,
               sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, y.data_ptr(), _rows(y, "y"),
               _DT[out_dtype], M, N, a.shape[1], row_amax.data_ptr() if row_amax is not None else None, _stream(a))
@@ -164,6 +202,7 @@ def gemm_quant(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b:
     returns (y bf16 [M, N], q e4m3fn [M, N], scale fp32 [M, 1])."""
     N = w.shape[0]
     M, sa, sa_st, sb, sb_st = _gemm_args(a, w, scale_a, scale_b, N)
+    _check_bias(bias, N, a.device)
     dev = a.device
     y = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
     amax = torch.empty((M,), device=dev, dtype=torch.float32)
@@ -177,31 +216,49 @@ def gemm_quant(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b:
 
 # ---- kernel 3 -------------------------------------------------------------------------------------------------------
 
-def gemm_swiglu(a: torch.Tensor, w_gate_up: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
-                bias: torch.Tensor | None = None, row_amax: torch.Tensor | None = None) -> torch.Tensor:
-    """fc1 + epilogue + SwiGLU in one kernel: bf16 h [M, F] from a [M, K] and the merged [2F, K] gate|up weight
-    (h3_tp2/fp8_swiglu.py:230-241)."""
+def _check_bias(bias: torch.Tensor | None, n: int, device: torch.device) -> None:
+    """A bf16 bias of n entries (kernel 3 reads 2F: gate then up), contiguous, on the operands' device."""
+    if bias is None:
+        return
+    if not isinstance(bias, torch.Tensor) or bias.dim() != 1 or bias.numel() != n or bias.dtype != torch.bfloat16 \
+            or bias.device != device or not bias.is_contiguous():
+        raise ValueError(f"bias must be a contiguous bfloat16 [{n}] vector on {device}")
+
+
+def _gate_up_width(w_gate_up: torch.Tensor) -> int:
     F2 = w_gate_up.shape[0]
     if F2 % 2:
         raise ValueError("gate/up weight must have an even number of rows")
-    F = F2 // 2
-    M, sa, sa_st, sb, sb_st = _gemm_args(a, w_gate_up, scale_a, scale_b, F2)
-    h = torch.empty((M, F), device=a.device, dtype=torch.bfloat16)
+    return F2 // 2
+
+def gemm_swiglu(a: torch.Tensor, w_gate_up: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                bias: torch.Tensor | None = None, row_amax: torch.Tensor | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """fc1 + epilogue + SwiGLU in one kernel: bf16 h [M, F] from a [M, K] and the merged [2F, K] gate|up weight
+    (h3_tp2/fp8_swiglu.py:230-241).  ``out``: a caller-supplied h (bf16 [M, F], rows contiguous)."""
+    F = _gate_up_width(w_gate_up)
+    M, sa, sa_st, sb, sb_st = _gemm_args(a, w_gate_up, scale_a, scale_b, 2 * F)
+    _check_bias(bias, 2 * F, a.device)
+    if row_amax is not None:
+        check_buffer(row_amax, "row_amax", (M,), torch.float32, a.device, contiguous=True)
+    h = out if out is not None else torch.empty((M, F), device=a.device, dtype=torch.bfloat16)
+    check_buffer(h, "out", (M, F), torch.bfloat16, a.device)
     _lib.call("h3fp8_gemm_swiglu", a.data_ptr(), _rows(a, "a"), w_gate_up.data_ptr(), _rows(w_gate_up, "w"),
               sa.data_ptr(), sa_st, sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, h.data_ptr(),
-              F, row_amax.data_ptr() if row_amax is not None else None, M, F, a.shape[1], _stream(a))
+              _rows(h, "out"), row_amax.data_ptr() if row_amax is not None else None, M, F, a.shape[1], _stream(a))
     return h
 
 
 def gemm_swiglu_quant(a: torch.Tensor, w_gate_up: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
                       bias: torch.Tensor | None = None, h_ws: torch.Tensor | None = None):
     """fc1 + SwiGLU + per-token requant (fp8_swiglu level 2, h3_tp2/fp8_swiglu.py:191-200): (q [M, F], scale [M, 1])."""
-    F2 = w_gate_up.shape[0]
-    F = F2 // 2
-    M, sa, sa_st, sb, sb_st = _gemm_args(a, w_gate_up, scale_a, scale_b, F2)
+    F = _gate_up_width(w_gate_up)
+    M, sa, sa_st, sb, sb_st = _gemm_args(a, w_gate_up, scale_a, scale_b, 2 * F)
+    _check_bias(bias, 2 * F, a.device)
     dev = a.device
     if h_ws is None:
         h_ws = torch.empty((M, F), device=dev, dtype=torch.bfloat16)
+    check_buffer(h_ws, "h_ws", (M, F), torch.bfloat16, dev, contiguous=True)   # the C side writes rows of F
     amax = torch.empty((M,), device=dev, dtype=torch.float32)
     q = torch.empty((M, F), device=dev, dtype=E4M3)
     s = torch.empty((M, 1), device=dev, dtype=torch.float32)
@@ -377,6 +434,7 @@ def scale_gate_rms_quant(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, 
     s_a, s_b = _product_args(x32, sa, sb, bias, M, H)
     res = residual_out if residual_out is not None else torch.empty((M, H), device=residual.device,
                                                                     dtype=torch.bfloat16)
+    check_buffer(res, "residual_out", (M, H), torch.bfloat16, residual.device)
     h = torch.empty((M, H), device=residual.device, dtype=torch.bfloat16) if modulated or not quant else None
     q = torch.empty((M, H), device=residual.device, dtype=E4M3) if quant else None
     s = torch.empty((M, 1), device=residual.device, dtype=torch.float32) if quant else None
@@ -405,6 +463,7 @@ def scale_indexed_gate(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bi
         raise ValueError(f"indices must be int32/int64 [{M}]")
     s_a, s_b = _product_args(x32, sa, sb, bias, M, H)
     o = out if out is not None else torch.empty((M, H), device=x.device, dtype=torch.bfloat16)
+    check_buffer(o, "out", (M, H), torch.bfloat16, x.device)
     _lib.call("h3fp8_scale_indexed_gate", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), s_b.data_ptr(),
               bias.data_ptr() if bias is not None else None, x.data_ptr(), _rows(x, "x"), gate.data_ptr(),
               _rows(gate, "gate"), gate.shape[0], indices.data_ptr(), indices.stride(0), indices.element_size(), M, H,
@@ -443,7 +502,13 @@ def scale_bias_cast(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias:
     _need_cuda(x32, sa, sb)
     M, N = x32.shape
     s_a, sa_st, s_b, sb_st = _epi_scales(x32, sa, sb, N)
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"scale_bias_cast writes bf16 or fp16, got {out_dtype}")
+    if bias is not None and (bias.dim() != 1 or bias.numel() != N or bias.dtype != out_dtype
+                             or bias.device != x32.device or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous [N] vector in the output dtype")
     y = out if out is not None else torch.empty((M, N), device=x32.device, dtype=out_dtype)
+    check_buffer(y, "out", (M, N), out_dtype, x32.device)
     _lib.call("h3fp8_scale_bias_cast", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), sa_st, s_b.data_ptr(),
               sb_st, bias.data_ptr() if bias is not None else None, y.data_ptr(), _rows(y, "y"), _DT[out_dtype], M, N,
               _stream(x32))

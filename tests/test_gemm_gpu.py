@@ -107,6 +107,22 @@ def test_fused_row_amax_and_quant(cuda, M, N, K):
     assert_quant_equal(q, s, *oracle_quant(y2.cpu()))
 
 
+@pytest.mark.parametrize("bias", [False, True])
+def test_fused_row_amax_fp16_output(cuda, bias):
+    """The row maxima of an fp16 output are the fp32 values of its largest rounded entries (not its bits read as
+    bf16), with values beyond the bf16-looking range of the fp16 bit patterns (|y| up to ~6e4) and a bias."""
+    from h3_tp2_amd import ops
+    M, N, K = 700, 1040, 512
+    a, w, sa, sb = serving_like(M, N, K, seed=23, device=cuda)
+    sa = sa * torch.exp2(torch.randint(-6, 14, (M,), generator=torch.Generator().manual_seed(3))).to(cuda)
+    bb = (torch.randn(N, generator=torch.Generator().manual_seed(4)) * 3).to(torch.float16).to(cuda) if bias else None
+    amax = torch.full((M,), 5.0, device=cuda)
+    y = ops.gemm(a, w, sa, sb, torch.float16, bias=bb, row_amax=amax)
+    torch.cuda.synchronize()
+    assert torch.equal(amax, y.float().abs().amax(dim=1))
+    assert np.array_equal(bits16(ops.gemm(a, w, sa, sb, torch.float16, bias=bb)), bits16(y))
+
+
 def test_grouped_matches_single(cuda):
     from h3_tp2_amd import ops
     shapes = [(2, 3072, 18432), (512, 4096, 6144), (1600, 1536, 4608), (300, 3072, 1040)]

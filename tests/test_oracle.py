@@ -539,3 +539,53 @@ def test_qk_head_sum_order_is_pinned():
         return O.bf16_bits_from_f32(np.array([np.float32(x[ORDER_DIM] * r) * np.float32(ORDER_W)], np.float32))[0]
     assert out[0, 0, ORDER_DIM] == norm(s8)
     assert norm(s8) != norm(s32)
+
+
+# ---- the torch restatement of the reference's CPU path (the CPU baseline leg of bench.py) ---------------------------
+from oracle import torch_path as TP  # noqa: E402
+
+
+def test_torch_path_quant_equals_the_oracle():
+    """quant_torch's torch ops give the C oracle's fp8 bytes and scales: seeded rows with outlier channels, the golden
+    fixture's rows, a zero row (MIN_SCALE) and inf / NaN rows."""
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(257, 3072, generator=g) * torch.exp(torch.randn(257, 1, generator=g) * 1.5)
+    x[:, :3] *= 40.0
+    x[5] = 0.0
+    x[7, 11] = float("inf")
+    x[9, 100] = float("nan")
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "quant.npz"))
+    for xb in (x.to(torch.bfloat16), torch.from_numpy(gold["x"].view(np.int16)).view(torch.bfloat16)):
+        q, s = TP.quant(xb)
+        qr, sr = O.quant_rows(xb.view(torch.int16).numpy().view(np.uint16))
+        nan_q = (qr & 0x7F) == 0x7F
+        qb = q.view(torch.uint8).numpy()
+        assert np.array_equal((qb & 0x7F) == 0x7F, nan_q) and np.array_equal(qb[~nan_q], qr[~nan_q])
+        sv = s.view(-1).numpy()
+        assert np.array_equal(np.isnan(sv), np.isnan(sr))
+        ok = ~np.isnan(sr)
+        assert np.array_equal(sv[ok].view(np.uint32), sr[ok].view(np.uint32))
+
+
+def test_torch_path_epilogue_and_swiglu_equal_the_oracle():
+    """epilogue_torch / swiglu_epilogue_torch's torch ops on one fp32 accumulator give the C oracle's bits (the SiLU
+    through torch's CPU exp, which agrees with the correctly rounded exp on every bf16 gate)."""
+    g = torch.Generator().manual_seed(32)
+    M, F = 193, 640
+    acc = torch.randn(M, 2 * F, generator=g) * 2000
+    acc[3, :5] = torch.tensor([0.0, -0.0, 1e-30, -1e-30, 3e4])
+    sa = torch.rand(M, generator=g) * 1e-3 + 1e-4
+    sb = torch.rand(2 * F, generator=g) * 1e-2 + 1e-3
+    y = TP.epilogue(acc, sa, sb)
+    assert np.array_equal(y.view(torch.int16).numpy().view(np.uint16), O.epilogue(acc.numpy(), sa.numpy(), sb.numpy()))
+    h = TP.swiglu(acc, sa, sb)
+    assert np.array_equal(h.view(torch.int16).numpy().view(np.uint16), O.scale_swiglu(acc.numpy(), sa.numpy(),
+                                                                                     sb.numpy()))
+
+
+def test_torch_path_product_exact_on_integers():
+    g = torch.Generator().manual_seed(33)
+    a = torch.randint(-4, 5, (64, 256), generator=g).float().to(torch.float8_e4m3fn)
+    w = torch.randint(-2, 3, (96, 256), generator=g).float().to(torch.float8_e4m3fn)
+    acc = TP.product(a, w)
+    assert np.array_equal(acc.numpy(), O.dequant_matmul(a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy()))
