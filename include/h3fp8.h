@@ -101,6 +101,23 @@ int h3fp8_gemm_quant(const void* a, int64_t lda, const void* w, int64_t ldw, con
                      int64_t K, float* amax_ws, void* q, int64_t ldq, float* scale, void* stream);
 
 /*
+ * h3fp8_gemm_quant without the workspace argument: the [M] row maxima go to a buffer the library owns (one static
+ * device array of H3FP8_NOALLOC_MAX_ROWS fp32 per device, 1 MiB, held until the process ends), so the call allocates
+ * nothing -- no hipMalloc / hipFree, no allocating library routine, no stream or event creation.  The buffer is
+ * cleared by a fill kernel on `stream` at every call.  Requirements beyond h3fp8_gemm_quant's: M <= H3FP8_NOALLOC_
+ * MAX_ROWS (H3FP8_EINVAL otherwise) and h3fp8_init already run on the current device (H3FP8_EINVAL otherwise).
+ * Every call on a device shares that device's buffer: calls that overlap on one device (on different streams, or
+ * from different threads) race and must be ordered by the caller.  Outputs y, q and scale equal h3fp8_gemm_quant's.
+ * No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).
+ */
+#define H3FP8_NOALLOC_MAX_ROWS 262144
+int h3fp8_gemm_quant_noalloc(const void* a, int64_t lda, const void* w, int64_t ldw, const float* sa,
+                             int64_t sa_stride, const float* sb, int64_t sb_stride, const void* bias, void* y,
+                             int64_t ldy, int64_t M, int64_t N, int64_t K, void* q, int64_t ldq, float* scale,
+                             void* stream);
+
+/*
  * Kernel 3 -- gate/up GEMM with the SwiGLU epilogue:  w_gate_up is [2F, K] (gate rows 0..F-1, up rows F..2F-1, vLLM's
  * merged layout), sb and bias are [2F].  For each (m, f):
  *   g = bf16(epi(acc[m, f])), u = bf16(epi(acc[m, F+f])), u = (u == 0 ? +0 : u),

@@ -118,10 +118,14 @@ int ensure_device_init() {
     void* p = nullptr;
     H3_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_h3_silu_table)));
     g_silu_ptr[dev] = (const uint16_t*)p;
+    const int rc = gemm_scratch_setup(dev);
+    if (rc) return rc;
     g_cus[dev] = cus > 0 ? cus : 1;
     g_inited[dev].store(true, std::memory_order_release);
     return H3FP8_OK;
 }
+
+bool device_ready(int dev) { return dev >= 0 && dev < kMaxDevices && g_inited[dev].load(std::memory_order_acquire); }
 
 int cu_count() {
     int dev = 0;

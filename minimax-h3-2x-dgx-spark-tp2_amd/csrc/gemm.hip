@@ -914,6 +914,31 @@ int quant_rows_amax_launch(const void* x, int64_t ldx, int64_t M, int64_t K, con
                            int64_t ldq, float* scale, hipStream_t st);
 }
 
+// ---- the library-owned row-maxima buffer of h3fp8_gemm_quant_noalloc -------------------------------------------------
+// One array per device (the loader gives every device its own copy at its own address), H3FP8_NOALLOC_MAX_ROWS fp32
+// row maxima = 1 MiB, held until the process ends.  Its name is a host-side stand-in: host code uses only the device
+// address that hipGetSymbolAddress returned for the device (g_scratch_ptr), never `scratch` itself.
+static __device__ __align__(256) float scratch[H3FP8_NOALLOC_MAX_ROWS];
+
+namespace {
+constexpr int kScratchDevices = 64;
+float* g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+namespace h3host {
+// Called once per device by the library's set-up (ensure_device_init), with that device current.
+int gemm_scratch_setup(int dev) {
+    if (dev < 0 || dev >= kScratchDevices) {
+        set_error("device index %d out of range", dev);
+        return H3FP8_EINVAL;
+    }
+    float* p = nullptr;
+    H3_CHECK_HIP(hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = p;
+    return H3FP8_OK;
+}
+}  // namespace h3host
+
 extern "C" {
 
 int h3fp8_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const float* sa, int64_t sa_stride,
@@ -945,6 +970,32 @@ int h3fp8_gemm_quant(const void* a, int64_t lda, const void* w, int64_t ldw, con
                         stream);
     if (rc) return rc;
     return h3host::quant_rows_amax_launch(y, ldy, M, N, amax_ws, q, ldq, scale, (hipStream_t)stream);
+}
+
+int h3fp8_gemm_quant_noalloc(const void* a, int64_t lda, const void* w, int64_t ldw, const float* sa,
+                             int64_t sa_stride, const float* sb, int64_t sb_stride, const void* bias, void* y,
+                             int64_t ldy, int64_t M, int64_t N, int64_t K, void* q, int64_t ldq, float* scale,
+                             void* stream) {
+    H3_REQUIRE(M >= 0 && M <= H3FP8_NOALLOC_MAX_ROWS,
+               "h3fp8_gemm_quant_noalloc: M = %lld rows exceeds the library buffer's %d (use h3fp8_gemm_quant with a "
+               "workspace)", (long long)M, H3FP8_NOALLOC_MAX_ROWS);
+    H3_REQUIRE(M == 0 || (q && scale), "h3fp8_gemm_quant_noalloc: null output");
+    int rc = check_gemm(a, lda, w, ldw, sa, sa_stride, sb, sb_stride, y, ldy, M, N, K, N, "h3fp8_gemm_quant_noalloc");
+    if (rc) return rc;
+    if (M == 0 || N == 0) return H3FP8_OK;
+    // no set-up here (it creates a stream and waits): the caller has run h3fp8_init on this device
+    int dev = -1;
+    H3_CHECK_HIP(hipGetDevice(&dev));
+    H3_REQUIRE(h3host::device_ready(dev) && dev < kScratchDevices && g_scratch_ptr[dev],
+               "h3fp8_gemm_quant_noalloc: call h3fp8_init on device %d first", dev);
+    float* amax = g_scratch_ptr[dev];
+    hipStream_t st = (hipStream_t)stream;
+    rc = zero_rows(amax, M, st);                        // a fill kernel: also safe under stream capture
+    if (rc) return rc;
+    rc = run_gemm(EPI_AMAX, (const uint8_t*)a, lda, (const uint8_t*)w, ldw, sa, sa_stride, sb, sb_stride, bias, y, ldy,
+                  H3FP8_DT_BF16, M, N, K, N, amax, nullptr, st);
+    if (rc) return rc;
+    return h3host::quant_rows_amax_launch(y, ldy, M, N, amax, q, ldq, scale, st);
 }
 
 int h3fp8_gemm_swiglu(const void* a, int64_t lda, const void* w_gate_up, int64_t ldw, const float* sa,

@@ -132,6 +132,8 @@ namespace h3host {
 void set_error(const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 int ensure_device_init();                      // per-device one-time set-up (SiLU table); returns status
+bool device_ready(int dev);                    // has ensure_device_init completed on device dev (no side effects)
+int gemm_scratch_setup(int dev);               // the device address of gemm.hip's row-maxima buffer (set-up only)
 const uint16_t* silu_table_ptr();              // device address of the current device's SiLU table
 int cu_count();                                // compute units of the current device (after ensure_device_init)
 }  // namespace h3host

@@ -17,6 +17,7 @@ H3FP8_DT_BF16 = 0
 H3FP8_DT_FP16 = 1
 H3FP8_DT_F32 = 2
 MAX_GROUPS = 8
+NOALLOC_MAX_ROWS = 262144       # H3FP8_NOALLOC_MAX_ROWS
 
 _lib = None
 _lock = threading.Lock()
@@ -41,6 +42,7 @@ _SIGS = {
     "h3fp8_quant_segments": ([P, I64, I64, I64, I64, I64, P, I64, P, P], I),
     "h3fp8_gemm": ([P, I64, P, I64, P, I64, P, I64, P, P, I64, I, I64, I64, I64, P, P], I),
     "h3fp8_gemm_quant": ([P, I64, P, I64, P, I64, P, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P], I),
+    "h3fp8_gemm_quant_noalloc": ([P, I64, P, I64, P, I64, P, I64, P, P, I64, I64, I64, I64, P, I64, P, P], I),
     "h3fp8_gemm_swiglu": ([P, I64, P, I64, P, I64, P, I64, P, P, I64, P, I64, I64, I64, P], I),
     "h3fp8_gemm_swiglu_quant": ([P, I64, P, I64, P, I64, P, I64, P, I64, I64, I64, P, P, P, I64, P, P], I),
     "h3fp8_scale_swiglu": ([P, I64, P, I64, P, I64, P, I64, I64, P, I64, P], I),
