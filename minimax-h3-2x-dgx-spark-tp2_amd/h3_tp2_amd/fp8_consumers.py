@@ -1,9 +1,10 @@
 """The GEMM-output stash protocol of the DiT block on MI355X (the consumer side of the dispatcher's stash hooks).
 
-Mirrors the reference's h3_tp2/fp8_consumers.py protocol -- ``Stash`` (:388-399), ``scale_pass_into`` (:373-380),
-``_product_fp32`` (:518-523), ``_vec`` (:526-528), ``stash_hook`` (:531-546), ``_materialize_all`` (:549-555),
-``_take`` (:640-648), the consumer wrappers (:651-747), ``block_plan`` (:758-784), ``make_block_forward`` (:787-808),
-``parse_sites`` (:811-819), ``install`` (:859-916) -- on the HIP kernels:
+The same protocol and names as the reference's h3_tp2/fp8_consumers.py (``Stash`` :388-399, ``scale_pass_into``
+:373-380, ``stash_hook`` :531-546, the consumer wrappers :651-747, ``block_plan`` :758-784, ``make_block_forward``
+:787-808, ``parse_sites`` :811-819, ``install`` :859-916), built here on a block scope object (``ConsumerScope``), one
+self-checked fused-consumer class for the three sites and the shared verdict book of ``_sites``; compute on the HIP
+kernels:
 
 * at the dispatcher's two-pass level ("tensor32"), a GEMM on the qkv / out / fc2 weight of the running block keeps its
   fp32 product (kernel 2, raw-accumulator mode) and its epilogue operands in a ``Stash``; the layer receives an
@@ -37,7 +38,7 @@ from typing import Any, Callable
 
 import torch
 
-from . import fp8_gemm
+from . import _sites, fp8_gemm
 
 logger = logging.getLogger("h3_tp2_amd.fp8_consumers")
 
@@ -47,17 +48,12 @@ HEAD_DIM = 128
 ROTARY_DIM = 96
 _SELFCHECK_ROWS = 64
 
-_tls = threading.local()   # ctx: the _Ctx of the DiT block whose forward is running in this thread
+_tls = threading.local()   # ctx: the ConsumerScope of the DiT block whose forward is running in this thread
+# checked / disabled: the verdict book of the self-checks; fused: site -> registered fused consumer
 _state: dict[str, Any] = {"sites": (), "disabled": set(), "fused": {}, "checked": {}}
 _stats = {"stash": 0, "fused": 0, "materialize": 0, "stock": 0, "fused_qkv": 0, "fused_out": 0, "fused_fc2": 0,
           "selfcheck_pass": 0, "selfcheck_fail": 0}
-_warned: set = set()
-
-
-def _warn_once(key: str, msg: str, *args: Any) -> None:
-    if key not in _warned:
-        _warned.add(key)
-        logger.warning("h3_tp2_amd fp8 consumers: " + msg, *args)
+_notes = _sites.Notes(logger, "h3_tp2_amd fp8 consumers: ")
 
 
 def scale_pass_into(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
@@ -75,60 +71,76 @@ class Stash:
         self.x32, self.sa, self.sb, self.bias, self.ph = x32, sa, sb, bias, ph
 
     def materialize(self) -> torch.Tensor:
+        """Write the stock output (the scale pass) into the placeholder and return it."""
         return scale_pass_into(self.x32, self.sa, self.sb, self.bias, self.ph)
 
     def rows(self, r: int) -> "Stash":
+        """The first r rows as a stash of their own (its own placeholder): the self-checks' sample."""
         return Stash(self.x32[:r], self.sa[:r], self.sb, self.bias, torch.empty_like(self.ph[:r]))
 
 
-class _Ctx:
+class ConsumerScope:
+    """One DiT block's forward: the weights whose GEMMs may be stashed (``want``: weight key -> site, each taken at most
+    once) and the stashes waiting for their consumers (``pending``: site -> Stash)."""
     __slots__ = ("want", "pending")
 
     def __init__(self, want: dict):
-        self.want = want          # (weight data_ptr, weight shape) -> site
+        self.want = want
         self.pending: dict[str, Stash] = {}
+
+    def flush(self, reason: str) -> None:
+        """Materialise every waiting stash: their consumers will run the stock way."""
+        for site, st in list(self.pending.items()):
+            st.materialize()
+            _stats["materialize"] += 1
+            _notes.once("mat-" + reason, "%s: stash of %s materialised, stock consumer", reason, site)
+        self.pending.clear()
+
+    def claim(self, site: str) -> Stash | None:
+        """The stash waiting for ``site``'s consumer (it stays registered until ``settle``); a consumer that finds only
+        other sites' stashes makes them real first."""
+        if not self.pending:
+            return None
+        st = self.pending.get(site)
+        if st is None:
+            self.flush(f"{site} consumer saw another site's stash")
+        return st
+
+    def settle(self, site: str) -> None:
+        self.pending.pop(site, None)
+
+
+_Ctx = ConsumerScope          # the name the protocol tests address
+
+
+def _scope() -> ConsumerScope | None:
+    return getattr(_tls, "ctx", None)
 
 
 def _vec(scale: torch.Tensor, n: int) -> torch.Tensor:
-    s = scale.reshape(-1).float()
-    return (s.expand(n) if s.numel() == 1 else s).contiguous()
+    flat = scale.reshape(-1).float()
+    return flat.expand(n).contiguous() if flat.numel() == 1 else flat.contiguous()
 
 
 def stash_hook(a, b, scale_a, scale_b, out_dtype, bias):  # noqa: ANN001
     """Dispatcher stash hook: when ``b`` is the qkv / out / fc2 weight of the running block (and the dispatcher runs
     the two-pass level), keep the fp32 product and return an uninitialised placeholder."""
-    ctx = getattr(_tls, "ctx", None)
-    if ctx is None or out_dtype is not torch.bfloat16 or fp8_gemm._state.get("fused"):
+    scope = _scope()
+    if scope is None or out_dtype is not torch.bfloat16 or fp8_gemm._state.get("fused"):
         return None
-    site = ctx.want.pop((b.data_ptr(), tuple(b.shape)), None)
+    site = scope.want.pop(_sites_key(b), None)
     if site is None:
         return None
-    if ctx.pending:                       # a stash that was never consumed: make it real before the next one
-        _materialize_all(ctx, f"unconsumed stash before {site}")
+    scope.flush(f"unconsumed stash before {site}")
     M, N = a.shape[0], b.shape[1]
     ph = torch.empty((M, N), device=a.device, dtype=out_dtype)
-    ctx.pending[site] = Stash(fp8_gemm.product_fp32(a, b), _vec(scale_a, M), _vec(scale_b, N), bias, ph)
+    scope.pending[site] = Stash(fp8_gemm.product_fp32(a, b), _vec(scale_a, M), _vec(scale_b, N), bias, ph)
     _stats["stash"] += 1
     return ph
 
 
-def _materialize_all(ctx: _Ctx, reason: str) -> None:
-    for site, st in list(ctx.pending.items()):
-        st.materialize()
-        _stats["materialize"] += 1
-        _warn_once("mat-" + reason, "%s: stash of %s materialised, stock consumer", reason, site)
-    ctx.pending.clear()
-
-
-def _take(site: str):  # noqa: ANN202
-    """(ctx, the site's stash or None); another site's pending stash is materialised first."""
-    ctx = getattr(_tls, "ctx", None)
-    if ctx is None or not ctx.pending:
-        return ctx, None
-    st = ctx.pending.get(site)
-    if st is None:
-        _materialize_all(ctx, f"{site} consumer saw another site's stash")
-    return ctx, st
+def _sites_key(w: torch.Tensor) -> tuple:
+    return w.data_ptr(), tuple(w.shape)
 
 
 def set_fused(site: str, fn: Callable | None) -> None:
@@ -137,10 +149,11 @@ def set_fused(site: str, fn: Callable | None) -> None:
     runs).  ``None`` removes it."""
     if site not in SITES:
         raise ValueError(f"unknown consumer site {site!r}")
+    registry = _state["fused"]
     if fn is None:
-        _state["fused"].pop(site, None)
+        registry.pop(site, None)
     else:
-        _state["fused"][site] = fn
+        registry[site] = fn
 
 
 def make_consumer_wrapper(site: str, orig):  # noqa: ANN001,ANN201
@@ -148,17 +161,18 @@ def make_consumer_wrapper(site: str, orig):  # noqa: ANN001,ANN201
     call, otherwise the stash materialised and the stock consumer."""
     @functools.wraps(orig)
     def consumer(*args, **kwargs):  # noqa: ANN002,ANN003,ANN202
-        ctx, st = _take(site)
-        if st is not None:
-            fn = _state["fused"].get(site)
-            if fn is not None and site not in _state["disabled"]:
-                out = fn(st, *args, **kwargs)
-                if out is not None:
-                    del ctx.pending[site]
-                    _stats["fused"] += 1
-                    return out
-            _materialize_all(ctx, f"{site}: no fused consumer took the call")
-            _stats["stock"] += 1
+        scope = _scope()
+        st = scope.claim(site) if scope is not None else None
+        if st is None:
+            return orig(*args, **kwargs)
+        fused = None if site in _state["disabled"] else _state["fused"].get(site)
+        result = fused(st, *args, **kwargs) if fused is not None else None
+        if result is not None:
+            scope.settle(site)
+            _stats["fused"] += 1
+            return result
+        scope.flush(f"{site}: no fused consumer took the call")
+        _stats["stock"] += 1
         return orig(*args, **kwargs)
 
     consumer._h3_tp2_amd_consumer = True
@@ -202,231 +216,242 @@ def gate_fused(st: Stash, x: torch.Tensor, gate: torch.Tensor, indices: torch.Te
     return ops.scale_indexed_gate(st.x32, st.sa, st.sb, st.bias, x, gate, indices, out=out)
 
 
-def _bits(t: torch.Tensor) -> torch.Tensor:
-    t = t.contiguous()
-    return t.view({1: torch.uint8, 2: torch.int16, 4: torch.int32}[t.element_size()])
+# ---- when a fused consumer may take a call -------------------------------------------------------------------------
+# Each rule is (reason, predicate that is True when the call is acceptable); the first failing rule names the reason.
+
+def _first_failure(rules) -> str | None:  # noqa: ANN001
+    for reason, ok in rules:
+        if not ok():
+            return reason
+    return None
 
 
-def _selfcheck(key, fused_fn, stock_fn) -> bool:  # noqa: ANN001
-    """Once per (site, shape): fused vs the scale pass + stock consumer on the first rows, bit for bit; a mismatch (or
-    an exception) disables the site for the process."""
-    ok = _state["checked"].get(key)
-    if ok is not None:
-        return ok
-    try:
-        fused, stock = fused_fn(), stock_fn()
-        ok = len(fused) == len(stock) and all(
-            f.shape == s.shape and f.dtype == s.dtype and torch.equal(_bits(f), _bits(s)) for f, s in zip(fused, stock))
-    except Exception as exc:  # noqa: BLE001
-        logger.warning("h3_tp2_amd fp8 consumers: self-check %s raised %s: %s", key, type(exc).__name__, exc)
-        ok = False
-    _state["checked"][key] = ok
-    if ok:
-        _stats["selfcheck_pass"] += 1
-    else:
-        _stats["selfcheck_fail"] += 1
-        _state["disabled"].add(key[0])
-        logger.warning("h3_tp2_amd fp8 consumers: self-check %s not bit-identical to the scale pass + the stock "
-                       "consumer; site %s disabled", key, key[0])
-    return ok
-
-
-def _on_gpu(*ts: torch.Tensor) -> bool:
+def _same_cuda_device(*ts: torch.Tensor) -> bool:
     dev = ts[0].device
     return dev.type == "cuda" and all(isinstance(t, torch.Tensor) and t.device == dev for t in ts)
+
+
+def _is_view_of(x: torch.Tensor, base: torch.Tensor) -> bool:
+    return x.data_ptr() == base.data_ptr() and x.stride() == base.stride()
 
 
 def qk_mismatch(st: Stash, q, k, q_weight, k_weight, rope_table, head_dim, rotary_dim, interleaved) -> str | None:  # noqa: ANN001
     """None when (q, k) are exactly the q/k views of the stash's placeholder and the kernel takes the call
     (half-split, head_dim 128, rotary 96), else the reason."""
-    ph = st.ph
-    if interleaved:
-        return "interleaved"
-    if q.dim() != 3 or k.dim() != 3 or q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
-        return "q/k rank or dtype"
-    T, H, D = q.shape
-    Hk = k.shape[1]
-    N = ph.shape[1]
-    if T == 0 or ph.dim() != 2 or ph.shape[0] != T or k.shape != (T, Hk, D) or N != (H + 2 * Hk) * D:
-        return "shapes"
-    if not ph.is_contiguous() or not st.x32.is_contiguous() or st.x32.shape != ph.shape:
-        return "placeholder/product layout"
-    eq, ek = ph[:, :H * D].view(T, H, D), ph[:, H * D:(H + Hk) * D].view(T, Hk, D)
-    if q.data_ptr() != eq.data_ptr() or k.data_ptr() != ek.data_ptr() or q.stride() != eq.stride() \
-            or k.stride() != ek.stride():
-        return "q/k are not the split views of the qkv placeholder"
-    if D != HEAD_DIM or head_dim not in (None, D):
-        return "head_dim"
-    rot = rope_table.shape[-1] if rope_table.dim() == 2 else -1
-    if rot != ROTARY_DIM or rotary_dim not in (None, rot) or rope_table.shape != (T, rot) or rope_table.stride(1) != 1:
-        return "rotary"
-    if rope_table.dtype not in (torch.bfloat16, torch.float32) or q_weight.shape != (D,) or k_weight.shape != (D,) \
-            or q_weight.dtype != torch.bfloat16 or k_weight.dtype != torch.bfloat16:
-        return "rope table or norm weight dtype/shape"
-    if not _on_gpu(st.x32, q_weight, k_weight, rope_table):
-        return "device"
-    return None
+    ph, x32 = st.ph, st.x32
+
+    def ranks():
+        return q.dim() == 3 and k.dim() == 3 and q.dtype == k.dtype == torch.bfloat16
+
+    def shapes():
+        T, H, D = q.shape
+        Hk = k.shape[1]
+        return T > 0 and ph.dim() == 2 and ph.shape[0] == T and k.shape == (T, Hk, D) and ph.shape[1] == (H + 2 * Hk) * D
+
+    def views():
+        T, H, D = q.shape
+        Hk = k.shape[1]
+        return (_is_view_of(q, ph[:, :H * D].view(T, H, D))
+                and _is_view_of(k, ph[:, H * D:(H + Hk) * D].view(T, Hk, D)))
+
+    def rotary():
+        rot = rope_table.shape[-1] if rope_table.dim() == 2 else -1
+        return (rot == ROTARY_DIM and rotary_dim in (None, rot) and tuple(rope_table.shape) == (q.shape[0], rot)
+                and rope_table.stride(1) == 1)
+
+    def tables():
+        D = q.shape[-1]
+        return (rope_table.dtype in (torch.bfloat16, torch.float32) and q_weight.shape == (D,) and k_weight.shape == (D,)
+                and q_weight.dtype == k_weight.dtype == torch.bfloat16)
+
+    return _first_failure((
+        ("interleaved", lambda: not interleaved),
+        ("q/k rank or dtype", ranks),
+        ("shapes", shapes),
+        ("placeholder/product layout", lambda: ph.is_contiguous() and x32.is_contiguous() and x32.shape == ph.shape),
+        ("q/k are not the split views of the qkv placeholder", views),
+        ("head_dim", lambda: q.shape[-1] == HEAD_DIM and head_dim in (None, HEAD_DIM)),
+        ("rotary", rotary),
+        ("rope table or norm weight dtype/shape", tables),
+        ("device", lambda: _same_cuda_device(x32, q_weight, k_weight, rope_table)),
+    ))
+
+
+def _row_tables_ok(H: int, tables) -> bool:  # noqa: ANN001
+    """gate / shift / scale rows the kernels take: bf16 [B > 0, H] with unit column stride, 16-byte aligned rows."""
+    return all(t.dim() == 2 and t.stride(1) == 1 and t.dtype == torch.bfloat16 and t.shape[1] == H and t.shape[0] > 0
+               and (t.shape[0] == 1 or t.stride(0) % 8 == 0) and t.data_ptr() % 16 == 0 for t in tables)
 
 
 def rows_mismatch(st: Stash, x: torch.Tensor, branch: torch.Tensor, *others: torch.Tensor) -> str | None:
     """None when ``branch`` is exactly the stash's placeholder and ``x`` (the residual) a contiguous bf16 tensor of the
     same shape on the same device as the other operands (gate / shift / scale rows, then the indices)."""
-    ph = st.ph
-    if branch.data_ptr() != ph.data_ptr() or branch.shape != ph.shape or branch.stride() != ph.stride():
-        return "branch is not the placeholder"
-    if x.dim() != 2 or x.shape != ph.shape or x.dtype != torch.bfloat16 or not x.is_contiguous() \
-            or not ph.is_contiguous() or not st.x32.is_contiguous() or st.x32.shape != ph.shape:
-        return "residual shape/dtype/layout"
-    if x.shape[0] == 0:
-        return "no rows"
-    H = x.shape[1]
-    if H % 8 or H > 8192:
-        return "width"
-    for o in others[:-1]:
-        if o.dim() != 2 or o.stride(1) != 1 or o.dtype != torch.bfloat16 or o.shape[1] != H or o.shape[0] == 0 \
-                or (o.shape[0] > 1 and o.stride(0) % 8) or o.data_ptr() % 16:
-            return "gate/shift/scale layout"
-    idx = others[-1]
-    if idx.dim() != 1 or idx.shape[0] != x.shape[0] or idx.dtype not in (torch.int32, torch.int64):
-        return "indices"
-    if not _on_gpu(x, st.x32, *others):
-        return "device"
-    return None
+    ph, x32 = st.ph, st.x32
+    tables, idx = others[:-1], others[-1]
+    return _first_failure((
+        ("branch is not the placeholder", lambda: _is_view_of(branch, ph) and branch.shape == ph.shape),
+        ("residual shape/dtype/layout", lambda: x.dim() == 2 and x.shape == ph.shape and x.dtype == torch.bfloat16
+         and x.is_contiguous() and ph.is_contiguous() and x32.is_contiguous() and x32.shape == ph.shape),
+        ("no rows", lambda: x.shape[0] > 0),
+        ("width", lambda: x.shape[1] % 8 == 0 and x.shape[1] <= 8192),
+        ("gate/shift/scale layout", lambda: _row_tables_ok(x.shape[1], tables)),
+        ("indices", lambda: idx.dim() == 1 and idx.shape[0] == x.shape[0] and idx.dtype in (torch.int32, torch.int64)),
+        ("device", lambda: _same_cuda_device(x, x32, *others)),
+    ))
+
+
+class FusedConsumer:
+    """The fused consumer of one site: ``mismatch(st, *args, **kwargs)`` says why it cannot take a call (None: it can);
+    ``signature`` keys the once-per-process self-check, which runs ``sample_fused(st, r, ...)`` against
+    ``sample_stock(st, r, ...)`` on the first r rows; ``run(st, ...)`` computes the call."""
+
+    def __init__(self, site: str, mismatch, signature, sample_fused, sample_stock, run):  # noqa: ANN001
+        self.site = site
+        self.mismatch, self.signature = mismatch, signature
+        self.sample_fused, self.sample_stock, self.run = sample_fused, sample_stock, run
+
+    def __call__(self, st: Stash, *args, **kwargs):  # noqa: ANN002,ANN003,ANN204
+        reason = self.mismatch(st, *args, **kwargs)
+        if reason is not None:
+            _notes.once(f"{self.site}-{reason}", "%s consumer not fused (%s)", self.site, reason)
+            return None
+        r = min(_SELFCHECK_ROWS, st.ph.shape[0])
+        key = (self.site,) + self.signature(st, *args, **kwargs)
+        if not _sites.checked(_state, _stats, _notes, key, lambda: self.sample_fused(st, r, *args, **kwargs),
+                              lambda: self.sample_stock(st, r, *args, **kwargs)):
+            return None
+        out = self.run(st, *args, **kwargs)
+        _stats["fused_" + self.site] += 1
+        return out
+
+
+def _heads(q, k):  # noqa: ANN001,ANN202
+    return q.shape[1], k.shape[1], q.shape[-1]
 
 
 def make_fused_qk(orig):  # noqa: ANN001,ANN201
     """The qkv site's fused consumer (registered by ``install``): ``fused_qk_norm_rope``'s arguments after the stash."""
-    def fused(st, q, k, q_weight, k_weight, rope_table, eps, *, head_dim=None, rotary_dim=None, interleaved=False):  # noqa: ANN001,ANN202
-        reason = qk_mismatch(st, q, k, q_weight, k_weight, rope_table, head_dim, rotary_dim, interleaved)
-        if reason is not None:
-            _warn_once("qkv-" + reason, "qkv consumer not fused (%s)", reason)
-            return None
-        H, Hk, D = q.shape[1], k.shape[1], q.shape[-1]
-        r = min(_SELFCHECK_ROWS, q.shape[0])
+    def mismatch(st, q, k, q_weight, k_weight, rope_table, eps, *, head_dim=None, rotary_dim=None, interleaved=False):  # noqa: ANN001,ANN202
+        return qk_mismatch(st, q, k, q_weight, k_weight, rope_table, head_dim, rotary_dim, interleaved)
 
-        def _fused_sub():  # noqa: ANN202
-            return qk_norm_rope_fused(st.rows(r), H, Hk, D, q_weight, k_weight, rope_table[:r], eps)
+    def signature(st, q, k, q_weight, k_weight, rope_table, eps, **_):  # noqa: ANN001,ANN202,ANN003
+        return tuple(st.ph.shape[1:]), rope_table.dtype
 
-        def _stock_sub():  # noqa: ANN202
-            p = st.rows(r).materialize()
-            oq, ok_ = orig(p[:, :H * D].view(r, H, D), p[:, H * D:(H + Hk) * D].view(r, Hk, D), q_weight, k_weight,
-                           rope_table[:r], eps, head_dim=head_dim, rotary_dim=rotary_dim, interleaved=interleaved)
-            return oq, ok_, p[:, (H + Hk) * D:].view(r, Hk, D)
+    def sample_fused(st, r, q, k, q_weight, k_weight, rope_table, eps, **_):  # noqa: ANN001,ANN202,ANN003
+        return qk_norm_rope_fused(st.rows(r), *_heads(q, k), q_weight, k_weight, rope_table[:r], eps)
 
-        if not _selfcheck(("qkv", tuple(st.ph.shape[1:]), rope_table.dtype), _fused_sub, _stock_sub):
-            return None
-        out_q, out_k, _ = qk_norm_rope_fused(st, H, Hk, D, q_weight, k_weight, rope_table, eps)
-        _stats["fused_qkv"] += 1
-        return out_q, out_k
+    def sample_stock(st, r, q, k, q_weight, k_weight, rope_table, eps, **kw):  # noqa: ANN001,ANN202,ANN003
+        H, Hk, D = _heads(q, k)
+        flat = st.rows(r).materialize()
+        qs, ks, vs = flat[:, :H * D], flat[:, H * D:(H + Hk) * D], flat[:, (H + Hk) * D:]
+        oq, ok = orig(qs.view(r, H, D), ks.view(r, Hk, D), q_weight, k_weight, rope_table[:r], eps, **kw)
+        return oq, ok, vs.view(r, Hk, D)
 
-    return fused
+    def run(st, q, k, q_weight, k_weight, rope_table, eps, **_):  # noqa: ANN001,ANN202,ANN003
+        return qk_norm_rope_fused(st, *_heads(q, k), q_weight, k_weight, rope_table, eps)[:2]
+
+    return FusedConsumer("qkv", mismatch, signature, sample_fused, sample_stock, run)
+
+
+def _norm_weight_ok(weight: torch.Tensor, residual: torch.Tensor) -> bool:
+    return (weight.shape == (residual.shape[1],) and weight.dtype == torch.bfloat16 and weight.is_contiguous()
+            and weight.device == residual.device and weight.data_ptr() % 16 == 0)
 
 
 def make_fused_gate_rms(orig):  # noqa: ANN001,ANN201
     """The out site's fused consumer: ``indexed_gate_rms_norm_scale_shift``'s arguments after the stash."""
-    def fused(st, residual, gate, branch, weight, shift, scale, indices, eps):  # noqa: ANN001,ANN202
+    def mismatch(st, residual, gate, branch, weight, shift, scale, indices, eps):  # noqa: ANN001,ANN202
         reason = rows_mismatch(st, residual, branch, gate, shift, scale, indices)
-        if reason is None and (weight.shape != (residual.shape[1],) or weight.dtype != torch.bfloat16
-                               or not weight.is_contiguous() or weight.device != residual.device
-                               or weight.data_ptr() % 16):
-            reason = "norm weight"
-        if reason is not None:
-            _warn_once("out-" + reason, "out consumer not fused (%s)", reason)
-            return None
-        r = min(_SELFCHECK_ROWS, residual.shape[0])
+        return reason if reason is not None or _norm_weight_ok(weight, residual) else "norm weight"
 
-        def _fused_sub():  # noqa: ANN202
-            return gate_rms_fused(st.rows(r), residual[:r], gate, weight, shift, scale, indices[:r], eps)
+    def signature(st, residual, gate, branch, weight, *_):  # noqa: ANN001,ANN202,ANN002
+        return tuple(residual.shape[1:]), gate.dtype, weight.dtype
 
-        def _stock_sub():  # noqa: ANN202
-            p = st.rows(r).materialize()
-            return orig(residual[:r], gate, p, weight, shift, scale, indices[:r], eps)
+    def sample_fused(st, r, residual, gate, branch, weight, shift, scale, indices, eps):  # noqa: ANN001,ANN202
+        return gate_rms_fused(st.rows(r), residual[:r], gate, weight, shift, scale, indices[:r], eps)
 
-        if not _selfcheck(("out", tuple(residual.shape[1:]), gate.dtype, weight.dtype), _fused_sub, _stock_sub):
-            return None
-        res = gate_rms_fused(st, residual, gate, weight, shift, scale, indices, eps)
-        _stats["fused_out"] += 1
-        return res
+    def sample_stock(st, r, residual, gate, branch, weight, shift, scale, indices, eps):  # noqa: ANN001,ANN202
+        return orig(residual[:r], gate, st.rows(r).materialize(), weight, shift, scale, indices[:r], eps)
 
-    return fused
+    def run(st, residual, gate, branch, weight, shift, scale, indices, eps):  # noqa: ANN001,ANN202
+        return gate_rms_fused(st, residual, gate, weight, shift, scale, indices, eps)
+
+    return FusedConsumer("out", mismatch, signature, sample_fused, sample_stock, run)
 
 
 def make_fused_gate(orig):  # noqa: ANN001,ANN201
     """The fc2 site's fused consumer: ``indexed_gate``'s arguments after the stash."""
-    def fused(st, x, gate, other, indices):  # noqa: ANN001,ANN202
-        reason = rows_mismatch(st, x, other, gate, indices)
-        if reason is not None:
-            _warn_once("fc2-" + reason, "fc2 consumer not fused (%s)", reason)
-            return None
-        r = min(_SELFCHECK_ROWS, x.shape[0])
+    def mismatch(st, x, gate, other, indices):  # noqa: ANN001,ANN202
+        return rows_mismatch(st, x, other, gate, indices)
 
-        def _fused_sub():  # noqa: ANN202
-            return (gate_fused(st.rows(r), x[:r].contiguous(), gate, indices[:r], reuse_placeholder=False),)
+    def signature(st, x, gate, other, indices):  # noqa: ANN001,ANN202
+        return tuple(x.shape[1:]), gate.dtype
 
-        def _stock_sub():  # noqa: ANN202
-            p = st.rows(r).materialize()
-            return (orig(x[:r].contiguous(), gate, p, indices[:r]),)
+    def sample_fused(st, r, x, gate, other, indices):  # noqa: ANN001,ANN202
+        return (gate_fused(st.rows(r), x[:r].contiguous(), gate, indices[:r], reuse_placeholder=False),)
 
-        if not _selfcheck(("fc2", tuple(x.shape[1:]), gate.dtype), _fused_sub, _stock_sub):
-            return None
-        out = gate_fused(st, x, gate, indices)
-        _stats["fused_fc2"] += 1
-        return out
+    def sample_stock(st, r, x, gate, other, indices):  # noqa: ANN001,ANN202
+        return (orig(x[:r].contiguous(), gate, st.rows(r).materialize(), indices[:r]),)
 
-    return fused
+    def run(st, x, gate, other, indices):  # noqa: ANN001,ANN202
+        return gate_fused(st, x, gate, indices)
+
+    return FusedConsumer("fc2", mismatch, signature, sample_fused, sample_stock, run)
 
 
 FUSED_FACTORIES = {"qkv": make_fused_qk, "out": make_fused_gate_rms, "fc2": make_fused_gate}
 
 
+# ---- the block scope -------------------------------------------------------------------------------------------------
+
+def _layer_refusal(site: str, layer, lora_types) -> str | None:  # noqa: ANN001
+    """Why ``site``'s GEMM cannot be stashed (None: it can)."""
+    if layer is None or (lora_types and isinstance(layer, lora_types)):
+        return f"{site}: missing or LoRA-wrapped layer"
+    if getattr(layer, "tp_size", 1) != 1:
+        return f"{site}: tp_size != 1 (an all-reduce would read the placeholder)"
+    w = getattr(layer, "weight", None)
+    width = int(getattr(layer, "output_size_per_partition", 0) or 0)
+    if not (isinstance(w, torch.Tensor) and w.dtype == torch.float8_e4m3fn and w.dim() == 2 and w.shape[1] == width):
+        return f"{site}: weight is not an unpadded FP8 [K, N] tensor"
+    return None
+
+
 def block_plan(block, sites, lora_types=()) -> tuple[dict | None, str]:  # noqa: ANN001
     """{(weight data_ptr, weight shape): site} for this block's eligible GEMMs, or (None, reason)."""
-    try:
-        if torch.compiler.is_compiling():
-            return None, "torch.compile tracing"
-    except AttributeError:
-        pass
-    layers = {"qkv": getattr(getattr(block, "attn", None), "qkv_proj", None),
-              "out": getattr(getattr(block, "attn", None), "out_proj", None),
-              "fc2": getattr(getattr(block, "mlp", None), "fc2", None)}
-    want: dict = {}
-    for site in sites:
-        if site in _state["disabled"]:
-            continue
-        layer = layers[site]
-        if layer is None or (lora_types and isinstance(layer, lora_types)):
-            return None, f"{site}: missing or LoRA-wrapped layer"
-        if getattr(layer, "tp_size", 1) != 1:
-            return None, f"{site}: tp_size != 1 (an all-reduce would read the placeholder)"
-        w = getattr(layer, "weight", None)
-        n = int(getattr(layer, "output_size_per_partition", 0) or 0)
-        if not isinstance(w, torch.Tensor) or w.dtype != torch.float8_e4m3fn or w.dim() != 2 or w.shape[1] != n:
-            return None, f"{site}: weight is not an unpadded FP8 [K, N] tensor"
-        want[(w.data_ptr(), tuple(w.shape))] = site
+    if _sites.tracing():
+        return None, "torch.compile tracing"
+    live = [site for site in sites if site not in _state["disabled"]]
+    layers = {site: _sites.site_layer(block, site) for site in live}
+    for site in live:
+        reason = _layer_refusal(site, layers[site], lora_types)
+        if reason is not None:
+            return None, reason
+    want = {_sites_key(layers[site].weight): site for site in live}
     return (want or None), "no site left"
 
 
 def make_block_forward(orig_forward, sites, lora_types=()):  # noqa: ANN001,ANN201
+    """Run a DiT block's forward inside a ConsumerScope (thread-local; the enclosing scope comes back afterwards); a
+    stash still waiting when the block returns is materialised."""
     @functools.wraps(orig_forward)
     def forward(self, *args, **kwargs):  # noqa: ANN001,ANN202
         want, reason = block_plan(self, sites, lora_types)
         if want is None:
-            _warn_once("plan-" + reason, "block not planned (%s); stock path", reason)
+            _notes.once("plan-" + reason, "block not planned (%s); stock path", reason)
             return orig_forward(self, *args, **kwargs)
-        prev = getattr(_tls, "ctx", None)
-        ctx = _Ctx(want)
-        _tls.ctx = ctx
-        ok = False
+        scope, outer = ConsumerScope(want), _scope()
+        _tls.ctx = scope
+        finished = False
         try:
-            out = orig_forward(self, *args, **kwargs)
-            ok = True
-            return out
+            result = orig_forward(self, *args, **kwargs)
+            finished = True
         finally:
-            _tls.ctx = prev
-            if ctx.pending:
-                if ok:
-                    _materialize_all(ctx, "stash left at the end of the block")
-                ctx.pending.clear()
+            _tls.ctx = outer
+            if finished:
+                scope.flush("stash left at the end of the block")
+            scope.pending.clear()
+        return result
 
     forward._h3_tp2_amd_consumer = True
     return forward
@@ -434,45 +459,43 @@ def make_block_forward(orig_forward, sites, lora_types=()):  # noqa: ANN001,ANN2
 
 def parse_sites(value: str | None) -> tuple[str, ...]:
     """"1"/"all" = every site; a comma list of qkv,out,fc2; empty/"0"/"off" = none."""
-    v = (value or "").strip().lower()
-    if v in ("1", "all", "on", "true"):
-        return SITES
-    if not v or v in ("0", "off", "false"):
+    return _sites.parse_site_list(value, SITES)
+
+
+def _lora_base_types() -> tuple:
+    try:
+        from vllm.lora.layers import BaseLayerWithLoRA  # noqa: PLC0415
+    except ImportError:
         return ()
-    return tuple(s for s in SITES if s in {p.strip() for p in v.split(",")})
+    return (BaseLayerWithLoRA,)
 
 
 def install(sites=SITES, tr=None, *, lora_types=None, fused: bool = True) -> list[str]:  # noqa: ANN001
     """Wrap the block forward and the sites' consumers in the transformer module ``tr`` and register the stash hook;
     with ``fused`` also the fused consumer kernels of the sites.  Needs the dispatcher's two-pass level (at the
     default level there is no fp32 product to stash)."""
-    sites = tuple(s for s in SITES if s in sites)
-    if not sites:
+    chosen = tuple(site for site in SITES if site in sites)
+    if not chosen:
         return []
-    if fp8_gemm._state.get("level") != "tensor32" or fp8_gemm._state.get("fused"):
+    two_pass = fp8_gemm._state.get("level") == "tensor32" and not fp8_gemm._state.get("fused")
+    if not two_pass:
         logger.warning("h3_tp2_amd fp8 consumers: needs the dispatcher's two-pass level; skipped")
         return []
     if tr is None:
         from vllm_omni.diffusion.models.minimax_h3 import minimax_h3_transformer as tr  # noqa: PLC0415
-    if lora_types is None:
-        try:
-            from vllm.lora.layers import BaseLayerWithLoRA  # noqa: PLC0415
-            lora_types = (BaseLayerWithLoRA,)
-        except ImportError:
-            lora_types = ()
     block_cls = tr.MiniMaxH3DiTBlock
     if getattr(block_cls.forward, "_h3_tp2_amd_consumer", False):
         return list(_state["sites"])
-    for site in sites:
-        name = CONSUMERS[site]
-        orig = getattr(tr, name)
-        setattr(tr, name, make_consumer_wrapper(site, orig))
+    for site in chosen:
+        stock = getattr(tr, CONSUMERS[site])
+        setattr(tr, CONSUMERS[site], make_consumer_wrapper(site, stock))
         if fused:
-            set_fused(site, FUSED_FACTORIES[site](orig))
-    block_cls.forward = make_block_forward(block_cls.forward, sites, lora_types)
+            set_fused(site, FUSED_FACTORIES[site](stock))
+    block_cls.forward = make_block_forward(block_cls.forward, chosen,
+                                           _lora_base_types() if lora_types is None else lora_types)
     fp8_gemm.set_stash_hook(stash_hook)
-    _state["sites"] = sites
-    return list(sites)
+    _state["sites"] = chosen
+    return list(chosen)
 
 
 def stats() -> dict:

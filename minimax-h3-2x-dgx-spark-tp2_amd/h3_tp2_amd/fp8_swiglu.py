@@ -105,25 +105,32 @@ def probe_gemm_swiglu(device="cuda") -> bool:  # noqa: ANN001
 
 
 def _fc2_kernel_cls():  # noqa: ANN202
-    cls = _state["fc2_kernel_cls"]
-    if cls is not None:
-        return cls
-    try:
-        from vllm.model_executor.kernels.linear.scaled_mm.ScaledMMLinearKernel import (  # noqa: PLC0415
-            FP8ScaledMMLinearKernel)
-    except ImportError:
-        return None
-    _state["fc2_kernel_cls"] = FP8ScaledMMLinearKernel
-    return FP8ScaledMMLinearKernel
+    """vLLM's FP8ScaledMMLinearKernel class (looked up once; a caller without vLLM sets ``_state["fc2_kernel_cls"]``)."""
+    if _state["fc2_kernel_cls"] is None:
+        try:
+            from vllm.model_executor.kernels.linear.scaled_mm.ScaledMMLinearKernel import (  # noqa: PLC0415
+                FP8ScaledMMLinearKernel)
+        except ImportError:
+            return None
+        _state["fc2_kernel_cls"] = FP8ScaledMMLinearKernel
+    return _state["fc2_kernel_cls"]
+
+
+def _fc2_plain_kernel(fc2):  # noqa: ANN001,ANN202
+    """fc2's FP8 scaled-mm kernel when fc2 is the plain layer the model uses (one tensor-parallel rank, no bias added
+    by the layer), else None: only then may its input quant be skipped."""
+    kcls = _fc2_kernel_cls()
+    kernel = getattr(getattr(fc2, "quant_method", None), "fp8_linear", None)
+    plain = (getattr(fc2, "tp_size", 1) == 1 and getattr(fc2, "bias", None) is None
+             and not getattr(fc2, "skip_bias_add", False))
+    return kernel if kcls is not None and isinstance(kernel, kcls) and plain else None
 
 
 def _fc2_direct(fc2, q: torch.Tensor, scale: torch.Tensor, lead) -> torch.Tensor | None:  # noqa: ANN001
-    """fc2 on the pre-quantised input through its own scaled-mm kernel (its ``apply_weights`` would quantise again).
-    Only the plain case the model uses (tp 1, no bias, an FP8 scaled-mm kernel); otherwise None."""
-    kcls = _fc2_kernel_cls()
-    kernel = getattr(getattr(fc2, "quant_method", None), "fp8_linear", None)
-    if kcls is None or not isinstance(kernel, kcls) or getattr(fc2, "tp_size", 1) != 1 \
-            or getattr(fc2, "bias", None) is not None or getattr(fc2, "skip_bias_add", False):
+    """fc2 on a pre-quantised input through its own scaled-mm kernel (its ``apply_weights`` would quantise again), or
+    None when fc2 is not the plain layer or its weight does not take q's width."""
+    kernel = _fc2_plain_kernel(fc2)
+    if kernel is None:
         return None
     w, w_s, _, _ = kernel._get_layer_params(fc2)
     if w.shape[0] != q.shape[1]:
@@ -132,84 +139,111 @@ def _fc2_direct(fc2, q: torch.Tensor, scale: torch.Tensor, lead) -> torch.Tensor
                                   output_shape=[*lead, w.shape[1]])
 
 
+class Fc1Stash:
+    """What the stash hook kept of fc1: the GEMM's operands (kernel 3 computes the product) or, without kernel 3, its
+    fp32 product; the per-token / per-channel scale vectors and the bias.  Either form yields the MLP's hidden row h or
+    fc2's quantised input."""
+    __slots__ = ("source", "sa", "sb", "bias")
+
+    def __init__(self, source, sa: torch.Tensor, sb: torch.Tensor, bias):  # noqa: ANN001
+        self.source, self.sa, self.sb, self.bias = source, sa, sb, bias
+
+    @property
+    def fused(self) -> bool:
+        return isinstance(self.source, GemmOperands)
+
+    @property
+    def width(self) -> int:
+        return self.source.shape[1] // 2
+
+    def hidden(self) -> torch.Tensor:
+        """bf16 h [M, F]."""
+        _stats["fused" if self.fused else "x32"] += 1
+        if self.fused:
+            return gemm_swiglu(self.source.a, self.source.b, self.sa, self.sb, self.bias)
+        return scale_swiglu(self.source, self.sa, self.sb, self.bias)
+
+    def quantised(self):  # noqa: ANN201
+        """(fp8 h [M, F], fp32 per-token scale [M, 1])."""
+        _stats["fused_quant" if self.fused else "x32"] += 1
+        if self.fused:
+            return gemm_swiglu_quant(self.source.a, self.source.b, self.sa, self.sb, self.bias)
+        return scale_swiglu_quant(self.source, self.sa, self.sb, self.bias)
+
+
 def _stash_hook(a, b, scale_a, scale_b, out_dtype, bias):  # noqa: ANN001
-    """Dispatcher stash hook: when the MLP forward requested it, keep fc1's operands (or, without kernel 3, its fp32
-    product) and return an uninitialised placeholder of the output's shape."""
+    """Dispatcher stash hook: on the fc1 GEMM the MLP forward asked for (``_tls.stash_next``), keep an ``Fc1Stash`` in
+    ``_tls.stash`` and return an uninitialised bf16 placeholder of the output's shape.  A bf16 output of even width that
+    equals the layer's logical width (``_tls.expect_n``, 0 = unknown) qualifies; anything else declines and withdraws
+    the request, so the GEMM takes the ordinary path."""
     if not getattr(_tls, "stash_next", False) or out_dtype is not torch.bfloat16:
         return None
+    _tls.stash_next = False                            # one request, one GEMM
     M, N = a.shape[0], b.shape[1]
     expect = getattr(_tls, "expect_n", 0)
-    if N % 2 or (expect and N != expect):              # padded fc1 (N != the logical width): the ordinary path
-        _tls.stash_next = False
+    if N % 2 or (expect and N != expect):              # padded fc1: not the MLP's merged [gate | up] product
         return None
     sa, sb = fp8_gemm._vec_scales(scale_a, scale_b, M, N)
-    if _state["gemm_swiglu"]:
-        _tls.stash = (GemmOperands(a, b), sa, sb, bias)
-    else:
-        _tls.stash = (fp8_gemm.product_fp32(a, b), sa, sb, bias)
-    _tls.stash_next = False
-    return torch.empty((M, N), device=a.device, dtype=out_dtype)   # placeholder, never read
+    source = GemmOperands(a, b) if _state["gemm_swiglu"] else fp8_gemm.product_fp32(a, b)
+    _tls.stash = Fc1Stash(source, sa, sb, bias)
+    return torch.empty((M, N), device=a.device, dtype=out_dtype)
+
+
+class _Fc1Capture:
+    """Arms the stash request for the fc1 call made inside the ``with`` block and disarms it on the way out, whatever
+    happens; ``stash`` is what the hook kept (None: fc1 ran the ordinary way)."""
+
+    def __init__(self, fc1):  # noqa: ANN001
+        self.expect = int(getattr(fc1, "output_size_per_partition", 0) or 0)
+        self.stash: Fc1Stash | None = None
+
+    def __enter__(self) -> "_Fc1Capture":
+        _tls.stash, _tls.expect_n, _tls.stash_next = None, self.expect, True
+        return self
+
+    def __exit__(self, *exc) -> None:  # noqa: ANN002
+        self.stash = getattr(_tls, "stash", None)
+        _tls.stash, _tls.expect_n, _tls.stash_next = None, 0, False
 
 
 def _install_on(cls, *, level: int, lora_layer_type=()) -> bool:  # noqa: ANN001
-    """Wrap ``cls.forward`` (an MLP with ``fc1``, ``act_fn``, ``fc2``); False when already wrapped."""
+    """Wrap ``cls.forward`` (an MLP with ``fc1``, ``act_fn``, ``fc2``); False when already wrapped.
+
+    The wrapped forward runs fc1 under a stash capture.  Nothing captured: the stock activation and fc2.  Captured:
+    fc1's placeholder is dropped and the stash yields h for fc2 (level 1), or fc2's quantised input, which fc2's own
+    kernel then takes directly (level 2).  An MLP whose fc1 or fc2 carries a LoRA wrapper takes the stock forward (the
+    wrapper adds its delta to fc1's returned tensor, which the fused path discards), and so does a level-2 MLP whose fc2
+    is not the plain layer (the stock forward recomputes fc1: correct, slower)."""
     if getattr(cls, "_h3_tp2_amd_swiglu", False):
         return False
-    orig_forward = cls.forward
-    fuse_quant = level >= 2
+    stock_forward = cls.forward
+    to_fc2_input = level >= 2
+
+    def lora_wrapped(mlp) -> bool:  # noqa: ANN001
+        return bool(lora_layer_type) and any(isinstance(layer, lora_layer_type) for layer in (mlp.fc1, mlp.fc2))
 
     def forward(self, x):  # noqa: ANN001,ANN202
-        # A LoRA wrapper adds its delta to fc1's returned tensor (which the fused path discards) and level 2 bypasses
-        # fc2's wrapper: such MLPs take the ordinary path.
-        if lora_layer_type and (isinstance(self.fc1, lora_layer_type) or isinstance(self.fc2, lora_layer_type)):
-            return orig_forward(self, x)
-        _tls.stash_next = True
-        _tls.stash = None
-        _tls.expect_n = int(getattr(self.fc1, "output_size_per_partition", 0) or 0)
-        stash = None
-        try:
-            hidden, _ = self.fc1(x)
-            stash = _tls.stash
-        finally:
-            _tls.stash_next = False
-            _tls.stash = None
-            _tls.expect_n = 0
-        if stash is None:
+        if lora_wrapped(self):
+            return stock_forward(self, x)
+        with _Fc1Capture(self.fc1) as cap:
+            placeholder, _ = self.fc1(x)
+        if cap.stash is None:
             _stats["stock"] += 1
-            hidden = self.act_fn(hidden)
-        else:
-            lead = hidden.shape[:-1]
-            del hidden                                   # the placeholder was never written
-            x32, sa, sb, bias = stash
+            return self.fc2(self.act_fn(placeholder))[0]
+        lead = placeholder.shape[:-1]
+        del placeholder                                 # never written
+        stash, cap.stash = cap.stash, None
+        if to_fc2_input:
+            out = _fc2_direct(self.fc2, *stash.quantised(), lead)
+            if out is not None:
+                _stats["fc2_direct"] += 1
+                return out
+            _stats["fc2_redo"] += 1
             del stash
-            ops_in = isinstance(x32, GemmOperands)
-            if fuse_quant:
-                if ops_in:
-                    q, scale = gemm_swiglu_quant(x32.a, x32.b, sa, sb, bias)
-                    _stats["fused_quant"] += 1
-                else:
-                    q, scale = scale_swiglu_quant(x32, sa, sb, bias)
-                    _stats["x32"] += 1
-                del x32, sa, sb, bias
-                out = _fc2_direct(self.fc2, q, scale, lead)
-                if out is not None:
-                    _stats["fc2_direct"] += 1
-                    return out
-                del q, scale
-                # fc2 layout the direct call does not take: redo fc1 through the ordinary path (correct, slower)
-                _stats["fc2_redo"] += 1
-                hidden, _ = self.fc1(x)
-                hidden = self.act_fn(hidden)
-            elif ops_in:
-                hidden = gemm_swiglu(x32.a, x32.b, sa, sb, bias).view(*lead, x32.shape[1] // 2)
-                _stats["fused"] += 1
-                del x32, sa, sb, bias
-            else:
-                hidden = scale_swiglu(x32, sa, sb, bias).view(*lead, x32.shape[1] // 2)
-                _stats["x32"] += 1
-                del x32, sa, sb, bias
-        out, _ = self.fc2(hidden)
-        return out
+            return stock_forward(self, x)
+        h = stash.hidden().view(*lead, stash.width)
+        del stash                                       # the fp32 product (two-pass form) goes before fc2 allocates
+        return self.fc2(h)[0]
 
     cls.forward = forward
     cls._h3_tp2_amd_swiglu = True
