@@ -4,6 +4,8 @@ CPU mirrors in place of the kernels.  Mirrors what the reference's tests/test_fp
 (site subsets, a self-check mismatch disables the site, mode 0 failing falls back to mode 1)."""
 import threading
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -78,6 +80,9 @@ def _reference(inp):
 
 
 def _install(fuse, tr, sites=("qkv", "fc1"), **kw):
+    """The sites over the stand-in stock producers; the fused mirrors here share the stand-ins' arithmetic, so the
+    caller vouches for the self-check (the default leaves the reducing sites stock: test_default_install_...)."""
+    kw.setdefault("trust_selfcheck", True)
     return fuse.install(sites, kernel1=False, tr=tr, quant_cls=FakeQuantFP8, lora_types=(), **kw)
 
 
@@ -245,3 +250,86 @@ def test_own_producers_sit_below_the_fused_wrappers(fuse, monkeypatch):
 def test_producer_takes_rules():
     x, w, sh, sc, gt, idx = mod_inputs(8, 64, seed=2)
     assert not fq.producer_takes(x, w, (sh, sc), idx)                           # CPU tensors: never
+
+
+def test_default_install_keeps_the_reducing_sites_stock(fuse, caplog):
+    """Without own_producers and without the caller vouching for the stock reduction, the qkv / fc1 sites are not
+    wired (a warning says so) and the block runs the stock producers; the fc2 site would still be wired."""
+    tr = make_tr(standin_rms, standin_gate_rms)
+    with caplog.at_level("WARNING"):
+        assert fuse.install(("qkv", "fc1"), kernel1=False, tr=tr, quant_cls=FakeQuantFP8, lora_types=()) == []
+    assert "qkv stays stock" in caplog.text and "fc1 stays stock" in caplog.text
+    assert tr.rms_norm_indexed_scale_shift is standin_rms and tr.indexed_gate_rms_norm_scale_shift is standin_gate_rms
+    inp = _inputs()
+    ref_blk, ref_res = _reference(inp)
+    blk, res = _run(tr, inp)
+    assert torch.equal(res, ref_res) and _same(blk.attn.qkv_proj.seen[0], ref_blk.attn.qkv_proj.seen[0])
+    assert fuse.stats()["fused_qkv"] == 0 and fuse.stats()["selfcheck_pass"] == 0
+
+
+def _fp64_sum_rms_quant(x, weight, shift, scale, indices, eps, stock=None, ph=None):
+    """The producer kernel's arithmetic (squares summed in fp64, one rounding), through the oracle."""
+    from oracle import oracle as O
+    from _util import bits16
+    h, q, sc = O.rms_quant(bits16(x), bits16(weight), bits16(shift), bits16(scale), indices.numpy(), eps)
+    hb = torch.from_numpy(h.view("int16")).view(BF16)
+    if ph is not None:
+        ph.copy_(hb)
+    return torch.from_numpy(q).view(E4M3), torch.from_numpy(sc).view(-1, 1)
+
+
+def test_fp64_sum_against_the_fp32_standin_falls_back_cleanly(fuse, monkeypatch):
+    """The reference's torch stand-in (fp32 sum) as the stock producer, the kernel's fp64-sum arithmetic as the fused
+    one.  The two sums differ on about 40 % of the rows, the bf16 rows on about 1 % (a one-ulp move of the sum rarely
+    crosses a bf16 rounding boundary) and the fp8 row the QKV GEMM reads on about 0.05 % (the bf16 move must also cross
+    an e4m3 boundary).  With such a row among the self-check's sampled rows both modes fail, the qkv site is disabled
+    and the block's results equal the stock path's."""
+    from oracle import oracle as O
+    from _util import bits16
+    H1 = 1024
+    xp, w, sh, sc, gt, idxp = mod_inputs(3000, H1, seed=5)         # rows 193, 1352, 1376, 1829 differ in fp8
+    _, q_k, s_k = O.rms_quant(bits16(xp), bits16(w), bits16(sh), bits16(sc), idxp.numpy(), 1e-6)
+    q_s, s_s = O.quant_rows(bits16(standin_rms(xp, w, sh, sc, idxp, 1e-6)))
+    differ = np.nonzero((q_k != q_s).any(1) | (s_k.view(np.uint32) != s_s.view(np.uint32)))[0]
+    assert differ.size, "the pool must hold a row whose fp8 bytes differ between the two sums"
+    pick = torch.from_numpy(np.concatenate([differ[:1], np.setdiff1d(np.arange(96), differ[:1])[:95]]))
+    x, idx = xp[pick].contiguous(), idxp[pick].contiguous()
+    monkeypatch.setattr(fq, "rms_quant", _fp64_sum_rms_quant)
+    tr = make_tr(standin_rms, standin_gate_rms)
+    _install(fuse, tr, ("qkv",))
+    br = torch.zeros(96, H1, dtype=BF16)
+    blk = tr.MiniMaxH3DiTBlock(H1, w, w)
+    res = blk(x, br, sh, sc, gt, idx)
+    ref = make_tr(standin_rms, standin_gate_rms).MiniMaxH3DiTBlock(H1, w, w)
+    ref_res = ref(x, br, sh, sc, gt, idx)
+    assert torch.equal(res, ref_res) and _same(blk.attn.qkv_proj.seen[0], ref.attn.qkv_proj.seen[0])
+    s = fuse.stats()
+    assert s["fused_qkv"] == 0 and s["selfcheck_fail"] == 2 and "qkv" in fq._state["disabled"]
+
+
+def test_fp64_sum_rows_outside_the_sample_are_why_the_default_is_stock(fuse, monkeypatch):
+    """The same pair with the fp8-differing row past the 64 sampled rows: the self-check passes (mode 0: the sampled
+    rows' fp8 bytes agree) and the site engages, so that row's fp8 bytes differ from the stock path's.  This is the
+    case the default install avoids by keeping the reducing sites stock unless the producers are the library's own."""
+    from oracle import oracle as O
+    from _util import bits16
+    H1 = 1024
+    xp, w, sh, sc, gt, idxp = mod_inputs(3000, H1, seed=5)
+    _, q_k, s_k = O.rms_quant(bits16(xp), bits16(w), bits16(sh), bits16(sc), idxp.numpy(), 1e-6)
+    q_s, s_s = O.quant_rows(bits16(standin_rms(xp, w, sh, sc, idxp, 1e-6)))
+    differ = np.nonzero((q_k != q_s).any(1) | (s_k.view(np.uint32) != s_s.view(np.uint32)))[0]
+    same = np.setdiff1d(np.arange(200), differ)[:95]
+    pick = torch.from_numpy(np.concatenate([same, differ[:1]]))          # the differing row last (row 95)
+    x, idx = xp[pick].contiguous(), idxp[pick].contiguous()
+    monkeypatch.setattr(fq, "rms_quant", _fp64_sum_rms_quant)
+    tr = make_tr(standin_rms, standin_gate_rms)
+    _install(fuse, tr, ("qkv",))
+    br = torch.zeros(96, H1, dtype=BF16)
+    blk = tr.MiniMaxH3DiTBlock(H1, w, w)
+    blk(x, br, sh, sc, gt, idx)
+    ref = make_tr(standin_rms, standin_gate_rms).MiniMaxH3DiTBlock(H1, w, w)
+    ref(x, br, sh, sc, gt, idx)
+    assert fuse.stats()["fused_qkv"] == 1
+    (qa, sa), (qb, sb) = blk.attn.qkv_proj.seen[0], ref.attn.qkv_proj.seen[0]
+    rows_differ = ((qa.view(torch.uint8) != qb.view(torch.uint8)).any(1) | (sa != sb).view(-1)).nonzero().view(-1)
+    assert rows_differ.tolist() == [95]
