@@ -38,7 +38,7 @@ from typing import Any, Callable
 
 import torch
 
-from . import _sites, fp8_gemm
+from . import _drift, _sites, fp8_gemm
 
 logger = logging.getLogger("h3_tp2_amd.fp8_consumers")
 
@@ -470,10 +470,13 @@ def _lora_base_types() -> tuple:
     return (BaseLayerWithLoRA,)
 
 
-def install(sites=SITES, tr=None, *, lora_types=None, fused: bool = True) -> list[str]:  # noqa: ANN001
+def install(sites=SITES, tr=None, *, lora_types=None, fused: bool = True, check_source: bool = True,  # noqa: ANN001
+            reviewed: dict | None = None, modules: dict | None = None) -> list[str]:
     """Wrap the block forward and the sites' consumers in the transformer module ``tr`` and register the stash hook;
     with ``fused`` also the fused consumer kernels of the sites.  Needs the dispatcher's two-pass level (at the
-    default level there is no fp32 product to stash)."""
+    default level there is no fp32 product to stash).  With ``check_source`` a site is wired only when the upstream
+    functions it relies on fingerprint to the reviewed sources (``_drift``; ``reviewed`` / ``modules`` override the
+    table and the upstream modules)."""
     chosen = tuple(site for site in SITES if site in sites)
     if not chosen:
         return []
@@ -486,6 +489,10 @@ def install(sites=SITES, tr=None, *, lora_types=None, fused: bool = True) -> lis
     block_cls = tr.MiniMaxH3DiTBlock
     if getattr(block_cls.forward, "_h3_tp2_amd_consumer", False):
         return list(_state["sites"])
+    if check_source:
+        chosen = _drift.keep_sites("consumers", chosen, tr, _notes, reviewed, modules)
+        if not chosen:
+            return []
     for site in chosen:
         stock = getattr(tr, CONSUMERS[site])
         setattr(tr, CONSUMERS[site], make_consumer_wrapper(site, stock))

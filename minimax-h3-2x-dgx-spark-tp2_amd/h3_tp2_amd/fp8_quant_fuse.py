@@ -43,7 +43,7 @@ from typing import Any, Callable
 
 import torch
 
-from . import _sites, ops
+from . import _drift, _sites, ops
 
 logger = logging.getLogger("h3_tp2_amd.fp8_quant_fuse")
 
@@ -615,14 +615,17 @@ def _env_flag(name: str) -> bool:
 
 
 def install(sites=SITES, *, kernel1: bool = True, tr=None, quant_cls=None, act_cls=None,  # noqa: ANN001
-            lora_types=None, own_producers: bool | None = None, trust_selfcheck: bool = False) -> list[str]:
+            lora_types=None, own_producers: bool | None = None, trust_selfcheck: bool = False,
+            check_source: bool = True, reviewed: dict | None = None, modules: dict | None = None) -> list[str]:
     """Wrap ``QuantFP8.forward`` (kernel 1 for the dynamic per-token calls when ``kernel1``; stash consumption) and,
     for the wired producer sites among ``sites``, the block forward and the producers.  Returns the sites wired.
 
     ``own_producers`` (default: env H3_TP2_AMD_OWN_PRODUCERS=1) replaces the stock RMS-norm producers by the producer
     kernels without the quant, which makes the qkv / fc1 sites bit-identical to their stock by construction.  Without
     it those two sites are wired only with ``trust_selfcheck`` (the caller vouches that the stock producers reduce like
-    the kernels); otherwise they stay stock, with a warning (see the module docstring)."""
+    the kernels); otherwise they stay stock, with a warning (see the module docstring).  With ``check_source`` a site
+    is wired only when the upstream functions between its producer and its quant fingerprint to the reviewed sources
+    (``_drift``; ``reviewed`` / ``modules`` override the table and the upstream modules)."""
     if isinstance(sites, str):
         sites = parse_sites(sites)
     if quant_cls is None:
@@ -648,6 +651,10 @@ def install(sites=SITES, *, kernel1: bool = True, tr=None, quant_cls=None, act_c
         return []
     if tr is None:
         from vllm_omni.diffusion.models.minimax_h3 import minimax_h3_transformer as tr  # noqa: PLC0415
+    if check_source:
+        chosen = list(_drift.keep_sites("producers", chosen, tr, _notes, reviewed, modules))
+        if not chosen:
+            return []
     if "fc1" in chosen and getattr(tr.indexed_gate_rms_norm_scale_shift, "_h3_tp2_amd_consumer", False):
         _notes.once("site-fc1-consumer", "site fc1 skipped: the consumer hook owns indexed_gate_rms_norm_scale_shift")
         chosen.remove("fc1")

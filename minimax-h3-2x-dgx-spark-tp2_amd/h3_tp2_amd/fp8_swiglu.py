@@ -21,9 +21,10 @@ import threading
 
 import torch
 
-from . import fp8_gemm, ops
+from . import _drift, _sites, fp8_gemm, ops
 
 logger = logging.getLogger("h3_tp2_amd.fp8_swiglu")
+_notes = _sites.Notes(logger, "h3_tp2_amd fused SwiGLU: ")
 
 _tls = threading.local()
 # gemm_swiglu: kernel 3 passed its install check (otherwise fc1's fp32 product is stashed and the standalone pass runs);
@@ -245,19 +246,25 @@ def _install_on(cls, *, level: int, lora_layer_type=()) -> bool:  # noqa: ANN001
         del stash                                       # the fp32 product (two-pass form) goes before fc2 allocates
         return self.fc2(h)[0]
 
+    forward.__wrapped__ = stock_forward             # source fingerprints see the upstream forward through it
     cls.forward = forward
     cls._h3_tp2_amd_swiglu = True
     _state["level"] = level
     return True
 
 
-def install(level: int = 1, tr=None, check: bool = True) -> bool:  # noqa: ANN001
+def install(level: int = 1, tr=None, check: bool = True, *, check_source: bool = True,  # noqa: ANN001
+            reviewed: dict | None = None) -> bool:
     """Wrap ``MiniMaxH3MLP.forward`` of the transformer module ``tr`` (default: vLLM-Omni's MiniMax H3) and register
-    the stash hook.  With ``check`` kernel 3's install check decides between the fused GEMM and the fp32 stash."""
+    the stash hook.  With ``check`` kernel 3's install check decides between the fused GEMM and the fp32 stash.  With
+    ``check_source`` the MLP forward must fingerprint to the reviewed upstream source (``_drift``): the wrapper relies
+    on fc1's output reaching ``act_fn`` and then fc2 and nothing else."""
     if level not in (1, 2):
         raise ValueError(f"unknown SwiGLU level {level!r}")
     if tr is None:
         from vllm_omni.diffusion.models.minimax_h3 import minimax_h3_transformer as tr  # noqa: PLC0415
+    if check_source and not _drift.keep_sites("mlp", ("fc1",), tr, _notes, reviewed, modules={}):
+        return False
     try:
         from vllm.lora.layers import BaseLayerWithLoRA  # noqa: PLC0415
         lora = (BaseLayerWithLoRA,)

@@ -24,7 +24,7 @@ def _recv(P, M, hl, d, seed):
 @pytest.mark.parametrize("P,hl,d", [(2, 28, 128), (1, 24, 128), (4, 6, 128), (2, 12, 128)])
 @pytest.mark.parametrize("M", [1, 200, 4100])
 def test_quant_from_recv(cuda, P, hl, d, M):
-    from h3_tp2_amd import fp8_quant_fuse as fq, ulysses_outq as oq
+    from h3_tp2_amd import fp8_quant_fuse as fq, ops
     recv = _recv(P, M, hl, d, seed=M + P)
     if M > 3:
         recv[:, 1] = 0.0                                   # a zero row: the minimum scale
@@ -33,7 +33,7 @@ def test_quant_from_recv(cuda, P, hl, d, M):
     rows = recv.transpose(0, 1).reshape(M, P * hl * d)     # the unpacked out-projection input
     q_ref, s_ref = O.quant_rows(bits16(rows))
     rd = recv.to(cuda)
-    q, s = oq.quant_from_recv(rd)
+    q, s = ops.quant_from_recv(rd)
     torch.cuda.synchronize()
     assert q.shape == (M, P * hl * d) and s.shape == (M, 1)
     assert_quant_equal(q, s, q_ref, s_ref)
@@ -47,13 +47,13 @@ def test_quant_from_recv(cuda, P, hl, d, M):
 
 def test_quant_rows_contiguous_and_strided_layouts(cuda):
     """The same entry point on ordinary rows (stride_m = P * seg) and on rows with a stride past their width."""
-    from h3_tp2_amd import ulysses_outq as oq
+    from h3_tp2_amd import ops
     M, P, seg, pad = 300, 2, 1536, 64
     g = torch.Generator().manual_seed(3)
     x = (torch.randn(M, P * seg + pad, generator=g) * 3).to(BF16)
     q_ref, s_ref = O.quant_rows(bits16(x[:, :P * seg].contiguous()))
     xd = x.to(cuda)
-    q, s = oq.quant_rows(xd, M, P, seg, seg, P * seg + pad)
+    q, s = ops.quant_segments(xd, M, P, seg, seg, P * seg + pad)
     torch.cuda.synchronize()
     assert_quant_equal(q, s, q_ref, s_ref)
 

@@ -83,6 +83,7 @@ def _install(fuse, tr, sites=("qkv", "fc1"), **kw):
     """The sites over the stand-in stock producers; the fused mirrors here share the stand-ins' arithmetic, so the
     caller vouches for the self-check (the default leaves the reducing sites stock: test_default_install_...)."""
     kw.setdefault("trust_selfcheck", True)
+    kw.setdefault("check_source", False)         # the stand-in module is not the reviewed upstream
     return fuse.install(sites, kernel1=False, tr=tr, quant_cls=FakeQuantFP8, lora_types=(), **kw)
 
 
@@ -257,7 +258,8 @@ def test_default_install_keeps_the_reducing_sites_stock(fuse, caplog):
     wired (a warning says so) and the block runs the stock producers; the fc2 site would still be wired."""
     tr = make_tr(standin_rms, standin_gate_rms)
     with caplog.at_level("WARNING"):
-        assert fuse.install(("qkv", "fc1"), kernel1=False, tr=tr, quant_cls=FakeQuantFP8, lora_types=()) == []
+        assert fuse.install(("qkv", "fc1"), kernel1=False, tr=tr, quant_cls=FakeQuantFP8, lora_types=(),
+                            check_source=False) == []
     assert "qkv stays stock" in caplog.text and "fc1 stays stock" in caplog.text
     assert tr.rms_norm_indexed_scale_shift is standin_rms and tr.indexed_gate_rms_norm_scale_shift is standin_gate_rms
     inp = _inputs()
