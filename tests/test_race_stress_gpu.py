@@ -1,0 +1,91 @@
+"""Race stress of the GEMM kernels' hand-rolled stage release (fence-free barriers with explicit vmcnt / lgkmcnt waits):
+kernel 2 at the 960x576 QKV shape and kernel 3 at the 1344x768 FFN gate/up shape, launched again and again while a
+memory-bound co-runner (a 1 GiB device-to-device copy) runs on a second stream of the same (default) priority, so that
+the persistent workgroups meet unpredictable memory latencies and CU sharing.  Every output must equal the first one
+bit for bit (and the first must equal a launch with no co-runner).  The loop stops at the first mismatch and is
+bounded in time.  A LDS stage refilled before every wave finished reading it, or read before its loads landed, shows
+up here as a differing output under load -- the failure the reference found in its own kernel
+(results/20261103-cutlass-sm120/race.md, scripts/fp8_cutlass_stress.py).
+
+    python tests/test_race_stress_gpu.py [--seconds S]    (standalone: a longer soak, same checks)
+"""
+import os
+import sys
+import time
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SECONDS = float(os.environ.get("H3_RACE_SECONDS", "20"))
+
+
+def _operands(device):
+    from h3_tp2_amd import ops, synthetic
+    M2, K, N2 = 16740, 3072, 9216
+    M3, F = 31248, 8192
+    a2, s2 = ops.quant_rows(synthetic.activations(M2, K, seed=0, n_out=3).to(device))
+    w2, sw2 = ops.quant_rows(synthetic.weight(N2, K, seed=1).to(device))
+    a3, s3 = ops.quant_rows(synthetic.activations(M3, K, seed=2, n_out=3).to(device))
+    w3, sw3 = ops.quant_rows(synthetic.weight(2 * F, K, seed=3).to(device))
+    return (a2, w2, s2, sw2.view(-1)), (a3, w3, s3, sw3.view(-1))
+
+
+def run(seconds: float, device, log=print) -> dict:
+    """Alternate kernel 2 and kernel 3 launches under the co-runner for ``seconds``; returns counts, raises
+    AssertionError at the first output that differs from the first launch's."""
+    from h3_tp2_amd import ops
+    (a2, w2, s2, sw2), (a3, w3, s3, sw3) = _operands(device)
+    amax3 = torch.empty(a3.shape[0], device=device)
+    ref2 = ops.gemm(a2, w2, s2, sw2)
+    ref3 = ops.gemm_swiglu(a3, w3, s3, sw3, row_amax=amax3)
+    ref_amax3 = amax3.clone()
+    torch.cuda.synchronize()
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(3)
+    dst = torch.empty_like(src)
+    side = torch.cuda.Stream(device=device)                 # default priority, like the launch stream
+    main = torch.cuda.current_stream(device)
+    out2, out3 = torch.empty_like(ref2), torch.empty_like(ref3)
+    counts = {"kernel2": 0, "kernel3": 0, "co_runner_copies": 0}
+    t_end = time.time() + seconds
+    while time.time() < t_end:
+        side.wait_stream(main)
+        with torch.cuda.stream(side):                       # the co-runner, overlapping both GEMMs
+            for _ in range(3):
+                dst.copy_(src)
+        counts["co_runner_copies"] += 3
+        ops.gemm(a2, w2, s2, sw2, out=out2)
+        ops.gemm_swiglu(a3, w3, s3, sw3, row_amax=amax3, out=out3)
+        main.wait_stream(side)
+        ok2 = torch.equal(out2.view(torch.int16), ref2.view(torch.int16))
+        ok3 = torch.equal(out3.view(torch.int16), ref3.view(torch.int16)) and torch.equal(amax3, ref_amax3)
+        counts["kernel2"] += 1
+        counts["kernel3"] += 1
+        if not (ok2 and ok3):
+            bad2 = int((out2.view(torch.int16) != ref2.view(torch.int16)).sum())
+            bad3 = int((out3.view(torch.int16) != ref3.view(torch.int16)).sum())
+            raise AssertionError(f"output differs from the first launch after {counts}: kernel 2 {bad2} elements, "
+                                 f"kernel 3 {bad3} elements")
+        if counts["kernel2"] % 25 == 0:
+            log(f"race stress: {counts} equal so far", flush=True)
+    torch.cuda.synchronize()
+    return counts
+
+
+def test_gemm_stage_release_under_a_co_runner(cuda):
+    counts = run(SECONDS, cuda)
+    assert counts["kernel2"] >= 5 and counts["kernel3"] >= 5
+
+
+if __name__ == "__main__":
+    import argparse
+    here = os.path.dirname(os.path.abspath(__file__))
+    for p in (os.path.dirname(here), os.path.join(os.path.dirname(here), "minimax-h3-2x-dgx-spark-tp2_amd")):
+        sys.path.insert(0, p)
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--seconds", type=float, default=120.0)
+    args = ap.parse_args()
+    from h3_tp2_amd import ops
+    ops.init(0)
+    print(run(args.seconds, torch.device("cuda", 0)), flush=True)
