@@ -10,6 +10,9 @@
 // The bf16 SiLU of every bf16 gate value, one table per device (128 KiB), filled once by h3fp8_init.
 __device__ uint16_t g_h3_silu_table[65536];
 
+// The compact rotated-key copy of the table (see h3fp8_common.h), filled from it by h3fp8_init.
+__device__ uint16_t g_h3_silu_rot[H3_SILU_ROT_LEN];
+
 // Counters of the e4m3 conversion self-check.
 __device__ unsigned long long g_h3_cvt_counts[4];
 
@@ -19,6 +22,7 @@ std::mutex g_init_mu;
 constexpr int kMaxDevices = 64;
 std::atomic<bool> g_inited[kMaxDevices] = {};
 const uint16_t* g_silu_ptr[kMaxDevices] = {};   // device address of each device's copy of g_h3_silu_table
+const uint16_t* g_silu_rot_ptr[kMaxDevices] = {};   // ... and of g_h3_silu_rot
 int g_cus[kMaxDevices] = {};                    // compute units of each device (persistent GEMM grid size)
 }  // namespace
 
@@ -53,6 +57,13 @@ __global__ void __launch_bounds__(256) h3_build_silu_table_kernel() {
         r = h3::bf16_rne(s);
     }
     g_h3_silu_table[i] = (uint16_t)r;
+}
+
+__global__ void __launch_bounds__(256) h3_build_silu_rot_kernel() {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= H3_SILU_ROT_LEN) return;
+    const uint32_t k = H3_SILU_ROT_R0 + i;
+    g_h3_silu_rot[i] = g_h3_silu_table[((k & 1u) << 15) | (k >> 1)];
 }
 
 __global__ void __launch_bounds__(256) h3_selfcheck_e4m3_kernel() {
@@ -111,6 +122,7 @@ int ensure_device_init() {
     hipStream_t s;
     H3_CHECK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     hipLaunchKernelGGL(h3_build_silu_table_kernel, dim3(65536 / 256), dim3(256), 0, s);
+    hipLaunchKernelGGL(h3_build_silu_rot_kernel, dim3((H3_SILU_ROT_LEN + 255) / 256), dim3(256), 0, s);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     (void)hipStreamDestroy(s);
@@ -118,6 +130,8 @@ int ensure_device_init() {
     void* p = nullptr;
     H3_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_h3_silu_table)));
     g_silu_ptr[dev] = (const uint16_t*)p;
+    H3_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_h3_silu_rot)));
+    g_silu_rot_ptr[dev] = (const uint16_t*)p;
     const int rc = gemm_scratch_setup(dev);
     if (rc) return rc;
     g_cus[dev] = cus > 0 ? cus : 1;
@@ -137,6 +151,12 @@ const uint16_t* silu_table_ptr() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
     return g_silu_ptr[dev];
+}
+
+const uint16_t* silu_rot_ptr() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    return g_silu_rot_ptr[dev];
 }
 
 }  // namespace h3host

@@ -19,7 +19,7 @@
 //     stall the instruction stream);
 //   * persistent tile loop: the load cursor runs two k-steps ahead of the MFMAs across tile boundaries, so the next
 //     tile's first stages and its scales (DMA'd into one of three LDS scale sets) load while the current tile's last
-//     k-steps and its epilogue run; the epilogue stages its output in a separate 4 KiB area per wave;
+//     k-steps and its epilogue run; the epilogue stages its output in a separate area per wave;
 //   * LDS rows are 128 bytes; 16-byte chunk c of row r is stored at chunk c ^ swz(r), swz(r) = ((r >> 1) & 7) ^
 //     ((r & 1) << 2): eight consecutive rows (32 banks) and sixteen (64 banks) read at one logical chunk never share a
 //     bank (conflict-free ds_read_b128);
@@ -32,7 +32,11 @@
 //   * tile order: workgroups are spread over the 8 XCDs round-robin by the hardware, so the tile index is remapped to
 //     give every XCD a contiguous range of tiles, walked in groups of GROUP_M row tiles (L2 reuse of both operands).
 // SwiGLU variant: the weight tile is 128 gate rows f0.. and the 128 matching up rows F+f0..; each wave holds the gate
-// and up accumulators of the same (m, f) and applies fp8_swiglu.py:64-70 in registers.
+// and up accumulators of the same (m, f) and applies fp8_swiglu.py:64-70 in registers.  Its SiLU lookups go to a
+// compact copy of the bf16 SiLU table in LDS (the 8960 gates with 2.6e-9 <= |g| <= 88.5, keyed by the bf16 bits with
+// the sign rotated to the lowest bit so that both signs form one contiguous range); a pass of 32 tokens with any gate
+// outside that range (zeros, tinier, larger, inf, NaN -- the wave votes) reads the full table in global memory
+// instead.  Both give the same table entry, so the output does not depend on the path taken.
 #include <algorithm>
 
 #include "h3fp8_common.h"
@@ -63,6 +67,7 @@ struct GemmParams {
     void* y;                   // [M, N] (SwiGLU: [M, F])
     float* row_amax;           // EPI_AMAX / EPI_SWIGLU (may be null for SwiGLU)
     const uint16_t* silu;      // SwiGLU table
+    const uint16_t* silu_rot;  // its compact rotated-key copy (loaded into LDS)
     int64_t lda, ldw, ldy;
     int64_t sa_stride, sb_stride;
     int M, N, K;               // SwiGLU: N = F (output width)
@@ -161,19 +166,33 @@ __device__ __forceinline__ void dma4(v4u desc, uint32_t lds_base, uint32_t voff)
                  : "memory", "m0");
 }
 
-// ---- LDS layout of a workgroup (150 KiB of the 160 KiB) ----
+// ---- LDS layout of a workgroup ----
+//   kernel 2 (150.5 KiB of the 160 KiB):
 //   [0, 128 KiB)          two operand stages of 64 KiB (weight rows, then token rows, 128 bytes each)
 //   [128 KiB, 144 KiB)    epilogue staging, 4 KiB per wave: 32 token rows x 64 channels of bf16
 //   [144 KiB, 150 KiB)    three scale sets of 2 KiB: sa of the tile's 256 token rows, then sb of its 256 weight rows
 //   [150 KiB, +512)       a scratch slot for the scale loads of k-steps that do not start a tile
+//   kernel 3 (160 KiB): the same with 2 KiB of staging per wave (16 token rows per flush), and after the scratch slot
+//   the compact SiLU table (17 920 bytes), loaded once per workgroup ahead of the first stage.
 // The stages are never used by the epilogue, so the loads of the next tile run under it.
-constexpr int STAGING_PER_WAVE = 32 * 128;
-constexpr int STAGING_OFF = NSTAGE * STAGE_BYTES;
 constexpr int SCALE_SET = 2 * 256 * 4;
 constexpr int NSCALE = 3;
-constexpr int SCALES_OFF = STAGING_OFF + 4 * STAGING_PER_WAVE;
-constexpr int JUNK_OFF = SCALES_OFF + NSCALE * SCALE_SET;   // 512 bytes: target of the scale loads that are not needed
-constexpr int LDS_TOTAL = JUNK_OFF + 512;
+constexpr int SILU_LDS_BYTES = H3_SILU_ROT_LEN * 2;          // the compact SiLU table (kernel 3)
+static_assert(SILU_LDS_BYTES % 256 == 0, "the table loads in 256-byte pieces");
+
+// The layout per epilogue: kernel 3 stages 16 token rows per flush (2 KiB per wave) to make room for the compact SiLU
+// table, which brings its workgroup to the 160 KiB of the CU; the other forms stage 32 rows.
+template <int EPI>
+struct Lds {
+    static constexpr int STG_ROWS = (EPI == EPI_SWIGLU) ? 16 : 32;
+    static constexpr int STAGING_PER_WAVE = STG_ROWS * 128;
+    static constexpr int STAGING_OFF = NSTAGE * STAGE_BYTES;
+    static constexpr int SCALES_OFF = STAGING_OFF + 4 * STAGING_PER_WAVE;
+    static constexpr int JUNK_OFF = SCALES_OFF + NSCALE * SCALE_SET;   // 512 bytes: target of unneeded scale loads
+    static constexpr int SILU_OFF = JUNK_OFF + 512;
+    static constexpr int TOTAL = SILU_OFF + ((EPI == EPI_SWIGLU) ? SILU_LDS_BYTES : 0);
+};
+static_assert(Lds<EPI_SWIGLU>::TOTAL <= 160 * 1024 && Lds<EPI_PLAIN>::TOTAL <= 160 * 1024, "LDS of one CU");
 
 // Per-wave addressing of one tile's global -> LDS loads.
 struct Loader {
@@ -330,7 +349,7 @@ __device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, i
     I.c = c;
     I.ks = 0;
     I.valid = id < gp.total_tiles;
-    I.dsa = lds0 + SCALES_OFF + (uint32_t)(c % NSCALE) * SCALE_SET + 256u * (uint32_t)wave;
+    I.dsa = lds0 + Lds<EPI>::SCALES_OFF + (uint32_t)(c % NSCALE) * SCALE_SET + 256u * (uint32_t)wave;
     I.dsb = I.dsa + 1024u;
     if (!I.valid) {
         // past the last tile: the loads still run (every k-step has the same instruction stream and wait counts),
@@ -374,10 +393,11 @@ __device__ __forceinline__ void issue_stage(uint32_t stage, const Cursor& I, uin
 // The scales of the cursor's tile when its k-step starts the tile: wave w loads sa of token rows 64 w .. 64 w + 63
 // and sb of weight rows 64 w .. 64 w + 63 into scale set c % NSCALE (a scalar scale has stride 0 and fills every
 // entry).  At any other k-step the two loads read nothing and land in the scratch slot.
+template <int EPI>
 __device__ __forceinline__ void issue_scales(uint32_t lds0, const Cursor& I) {
     const bool real = I.valid && I.ks == 0;
-    dma4(I.L.rsa, real ? I.dsa : lds0 + JUNK_OFF, real ? I.L.sa_off : OOB);
-    dma4(I.L.rsb, real ? I.dsb : lds0 + JUNK_OFF + 256, real ? I.L.sb_off : OOB);
+    dma4(I.L.rsa, real ? I.dsa : lds0 + Lds<EPI>::JUNK_OFF, real ? I.L.sa_off : OOB);
+    dma4(I.L.rsb, real ? I.dsb : lds0 + Lds<EPI>::JUNK_OFF + 256, real ? I.L.sb_off : OOB);
 }
 
 template <int EPI, bool GROUPED, bool HALF = false>
@@ -428,7 +448,7 @@ __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const 
             barrier_nofence();                          // ... and every wave's: the stage is free
         }
         if (u > KS_REL && u <= KS_REL + 16) issue_one<EPI>(S, I.L, u - KS_REL - 1);
-        if (u == KS_REL + 9) issue_scales(lds0, I);
+        if (u == KS_REL + 9) issue_scales<EPI>(lds0, I);
         if (u == KS_PUB) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(ks_loads_before_pub()));   // k-step g+1 (and older) has landed
             barrier_nofence();
@@ -474,7 +494,7 @@ __device__ __forceinline__ void kstep_half(uint8_t* lds, uint32_t lds0, int g, c
 #pragma unroll
             for (int k = 3 * (u - HALF_REL - 1); k < 3 * (u - HALF_REL); ++k) {
                 if (k < 16) issue_one<EPI>(S, I.L, k);
-                else if (k == 16) issue_scales(lds0, I);
+                else if (k == 16) issue_scales<EPI>(lds0, I);
             }
         }
         if (u == HALF_PUB) {
@@ -488,6 +508,16 @@ __device__ __forceinline__ void kstep_half(uint8_t* lds, uint32_t lds0, int g, c
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+// Orders one wave's LDS accesses across its lanes: a lane's staging writes become visible to the other lanes' reads
+// that follow.  The wave's LDS accesses already complete in order, so this emits no wait; it is there for the compiler,
+// which under per-lane semantics may otherwise reorder or tail-duplicate lane-divergent writes past other lanes' reads
+// (the barrier is convergent: it cannot be moved into a divergent branch).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // max(m, |lo half|, |hi half|) of a packed bf16 pair, as fp32 bit patterns (the row maximum of the fused quant).
@@ -526,7 +556,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
     const int hi = lane >> 5;
     const int mj = lane & 31;
     const int mrow0 = tm * BM + wm * 128;               // first token row of the wave
-    const float* sa_l = reinterpret_cast<const float*>(lds + SCALES_OFF + set * SCALE_SET);
+    const float* sa_l = reinterpret_cast<const float*>(lds + Lds<EPI>::SCALES_OFF + set * SCALE_SET);
     const float* sb_l = sa_l + 256;
     if (OUT_DT == H3FP8_DT_F32) {
         // probe mode: the raw fp32 accumulators, scales / bias / rounding not applied (16-byte stores per lane)
@@ -547,7 +577,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                 }
         return;
     }
-    uint8_t* stg = lds + STAGING_OFF + wave * STAGING_PER_WAVE;
+    uint8_t* stg = lds + Lds<EPI>::STAGING_OFF + wave * Lds<EPI>::STAGING_PER_WAVE;
     // element (ml, cl) of the 32 x 64 staging tile: row ml, 16-byte chunk (cl / 8) ^ (ml % 8), 8-byte half (cl / 4) % 2
     auto put4 = [&](int ml, int cl, uint32_t lo, uint32_t h2) {
         const int ch = (cl >> 3) ^ (ml & 7);
@@ -593,12 +623,27 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                 sbg_v[t][q] = *reinterpret_cast<const v4f*>(sb_l + wn * 64 + 32 * t + 8 * q + 4 * hi);
                 sbu_v[t][q] = *reinterpret_cast<const v4f*>(sb_l + 128 + wn * 64 + 32 * t + 8 * q + 4 * hi);
             }
+        const uint16_t* silu_l = reinterpret_cast<const uint16_t*>(lds + Lds<EPI>::SILU_OFF);
+        // 16 staged token rows to their output rows: 16 bytes per lane, 8 rows per store instruction
+        auto flush16 = [&](int m0, int c0, int ncols) {
+            const int c = lane & 7;
+            const int col = c0 + c * 8;
+            v4u v[2];
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+                const int ml = it * 8 + (lane >> 3);
+                v[it] = *reinterpret_cast<const v4u*>(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+            }
+            const uint32_t off = (col < ncols) ? (uint32_t)(m0 + (lane >> 3)) * row2 + (uint32_t)col * 2u : OOB;
+#pragma unroll
+            for (int it = 0; it < 2; ++it)
+                __builtin_amdgcn_raw_buffer_store_b128(v[it], yr, off + (uint32_t)it * 8u * row2, 0, 0);
+        };
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = mrow0 + 32 * j + mj;
             const float sam = sa_j[j];
-            // gate and up of the pass rounded to bf16 (packed: gate low, up high), then every SiLU lookup of the pass
-            // issued before the first is used (one round trip to the table per pass)
+            // gate and up of the pass rounded to bf16 (packed: gate low, up high)
             uint32_t gu[2][4][4], sl[2][4][4];
 #pragma unroll
             for (int t = 0; t < 2; ++t)
@@ -623,13 +668,39 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                         gu[t][q][r] = cvt_bf16x2(gy, uy);
                     }
                 }
+            // bf16(g/(1+exp(-g))) of every gate of the pass: from the compact table in LDS when every key of the pass
+            // lies in its range (the rotated key clamped to the range equals the key), else from the full table
+            uint32_t key[2][4][4];
+            uint64_t outside = 0;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) sl[t][q][r] = p.silu[gu[t][q][r] & 0xffffu];   // bf16(g/(1+exp(-g)))
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t g = gu[t][q][r];
+                        const uint32_t rk = ((g << 1) & 0xfffeu) | ((g >> 15) & 1u);
+                        const uint32_t ck = min(max(rk, H3_SILU_ROT_R0), H3_SILU_ROT_R0 + H3_SILU_ROT_LEN - 1u);
+                        outside |= __ballot(ck != rk);
+                        key[t][q][r] = ck - H3_SILU_ROT_R0;
+                    }
+            if (outside == 0) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sl[t][q][r] = silu_l[key[t][q][r]];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sl[t][q][r] = p.silu[gu[t][q][r] & 0xffffu];
+            }
             uint32_t rmax = 0;
+            uint32_t hp[2][4][2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -642,13 +713,26 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                         const float u = zero_to_pos(u2f(gu[t][q][r] & 0xffff0000u));   // -0 up -> +0 (fp8_swiglu.py:66)
                         hv[r] = bf16_to_f32(sl[t][q][r]) * u;
                     }
-                    const uint32_t h01 = cvt_bf16x2(hv[0], hv[1]), h23 = cvt_bf16x2(hv[2], hv[3]);
-                    if (ok) rmax = max_abs_bf16x2(max_abs_bf16x2(rmax, h01), h23);
-                    put4(mj, cl, h01, h23);
+                    hp[t][q][0] = cvt_bf16x2(hv[0], hv[1]);
+                    hp[t][q][1] = cvt_bf16x2(hv[2], hv[3]);
+                    if (ok) rmax = max_abs_bf16x2(max_abs_bf16x2(rmax, hp[t][q][0]), hp[t][q][1]);
                 }
             }
             if (p.row_amax) row_amax(rmax, m);
-            flush(mrow0 + 32 * j, col0, F);
+            // the pass's 32 token rows through the 16-row staging area, one half at a time (this wave's LDS accesses
+            // complete in order, so the second half's writes follow the first half's reads)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                wave_sync();                            // the previous flush's reads before these writes
+                if ((mj >> 4) == half) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) put4(mj & 15, 32 * t + 8 * q + 4 * hi, hp[t][q][0], hp[t][q][1]);
+                }
+                wave_sync();                            // every lane's writes before any lane's reads
+                flush16(mrow0 + 32 * j + 16 * half, col0, F);
+            }
         }
     } else {
         const int col0 = wcol;
@@ -668,6 +752,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
             uint32_t rmax = 0;
 #pragma unroll
             for (int ip = 0; ip < NI / 2; ++ip) {
+                wave_sync();                            // the previous flush's reads before these writes
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii) {
                     const int i = 2 * ip + ii;
@@ -703,6 +788,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                         put4(mj, cl, lo, hi2);
                     }
                 }
+                wave_sync();                            // every lane's writes before any lane's reads
                 flush(mrow0 + 32 * j, col0 + 64 * ip, p.N);
             }
             if (EPI == EPI_AMAX) row_amax(rmax, m);
@@ -715,7 +801,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
 // next tile (and its scales) load while the current tile's last k-steps and epilogue run.
 template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED, bool HALF = false>
 __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_TOTAL];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[Lds<EPI>::TOTAL];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -732,11 +818,18 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     // prologue: k-steps 0 and 1 (and the scales of their tiles) in flight, the sub-step-0 fragments of k-step 0 in
     // registers; every load group is 16 stage loads followed by 2 scale loads
     v8i fa0[4], fb0[4], fa1[4], fb1[4];
+    if (EPI == EPI_SWIGLU) {
+        // the compact SiLU table into LDS, once per workgroup, ahead of the stage loads: the wait below for the
+        // first stage covers it (loads complete in order)
+        const v4u td = buffer_desc(gp.g[0].silu_rot, SILU_LDS_BYTES);
+        for (int ch = wave; ch < SILU_LDS_BYTES / 256; ch += 4)
+            dma4(td, lds0 + Lds<EPI>::SILU_OFF + (uint32_t)ch * 256u, (uint32_t)ch * 256u + 4u * (uint32_t)lane);
+    }
     issue_stage<EPI>(lds0, I, wofs);
-    issue_scales(lds0, I);
+    issue_scales<EPI>(lds0, I);
     cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
     issue_stage<EPI>(lds0 + STAGE_BYTES, I, wofs);
-    issue_scales(lds0, I);
+    issue_scales<EPI>(lds0, I);
     if (I.valid) cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(18));
     barrier_nofence();
@@ -901,6 +994,7 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
                               reinterpret_cast<uint8_t*>(y) + r0 * ldy * out_elem, ldy, Mi, N, K, w_rows,
                               row_amax ? row_amax + r0 : nullptr, silu, epi == EPI_SWIGLU);
         gp.n = 1;
+        if (epi == EPI_SWIGLU) gp.g[0].silu_rot = h3host::silu_rot_ptr();
         const int rc = launch_split(gp, epi, out_dt, bias != nullptr, st);
         if (rc) return rc;
     }

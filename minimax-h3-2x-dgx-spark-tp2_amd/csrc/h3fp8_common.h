@@ -14,6 +14,13 @@
 // vLLM's minimum per-token scale 1/(448*512) as an fp32 constant (fp8_quant_fuse.py:78-79): 0x36924925.
 #define H3_MIN_SCALE_BITS 0x36924925u
 
+// The compact SiLU table of kernel 3: entry i holds silu(g) of the bf16 g whose rotated key
+// ((bits << 1) & 0xfffe) | (bits >> 15) (the sign moved to the lowest bit) is H3_SILU_ROT_R0 + i.  The keys cover
+// |g| in [2.6e-9, 88.5] for both signs (8960 entries, 17920 bytes); every other g (zeros, tinier, larger, inf, NaN)
+// is looked up in the full table.
+#define H3_SILU_ROT_R0 0x6264u
+#define H3_SILU_ROT_LEN 8960
+
 namespace h3 {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -135,6 +142,7 @@ int ensure_device_init();                      // per-device one-time set-up (Si
 bool device_ready(int dev);                    // has ensure_device_init completed on device dev (no side effects)
 int gemm_scratch_setup(int dev);               // the device address of gemm.hip's row-maxima buffer (set-up only)
 const uint16_t* silu_table_ptr();              // device address of the current device's SiLU table
+const uint16_t* silu_rot_ptr();                // ... and of its compact rotated-key copy (kernel 3's LDS table)
 int cu_count();                                // compute units of the current device (after ensure_device_init)
 }  // namespace h3host
 

@@ -131,6 +131,51 @@ def test_gemm_swiglu_random_within_tolerance(cuda, M):
     check_close_swiglu(h, A @ W.T, sa, sb, abs_products(a, w))
 
 
+def _gate_sweep(gate_bits: np.ndarray, M: int, device):
+    """Kernel 3 operands whose accumulator is exactly 1 at every (m, n) (a[:, 0] = w[:, 0] = 1, zeros elsewhere), with
+    scale_a = 1, the gate column f's weight scale = the bf16 value gate_bits[f] (exact in fp32) and every up column's
+    weight scale 1: the gate of column f is that bf16 value and h = bf16(silu(g) * 1)."""
+    F, K = len(gate_bits), 128
+    a = torch.zeros(M, K)
+    a[:, 0] = 1
+    w = torch.zeros(2 * F, K)
+    w[:, 0] = 1
+    gates = torch.from_numpy(gate_bits.astype(np.uint16).view(np.int16)).view(torch.bfloat16).float()
+    sb = torch.cat([gates, torch.ones(F)])
+    return (a.to(torch.float8_e4m3fn).to(device), w.to(torch.float8_e4m3fn).to(device), torch.ones(M, device=device),
+            sb.to(device), np.ones((M, 2 * F), np.float32), np.ones(M, np.float32), sb.numpy())
+
+
+def test_gemm_swiglu_every_gate_bit_pattern(cuda):
+    """All 65536 bf16 gate values through kernel 3's SiLU lookup (zeros, subnormals, the compact LDS table's range and
+    both its edges, huge values, infinities, NaNs): passes whose gates all lie in the compact range take the LDS
+    table, the others the full table; either way the oracle's entry."""
+    from h3_tp2_amd import ops
+    a, w, sa, sb, acc, sa_np, sb_np = _gate_sweep(np.arange(65536), 64, cuda)
+    h = ops.gemm_swiglu(a, w, sa, sb)
+    torch.cuda.synchronize()
+    _nan_aware_equal(bits16(h), O.scale_swiglu(acc, sa_np, sb_np))
+
+
+def test_gemm_swiglu_compact_table_on_the_fast_path(cuda):
+    """Only gates inside the compact table's range (2.6e-9 <= |g| <= 88.5, both signs), laid out in its key order and
+    128 columns per weight tile, so every pass of every wave stays on the LDS path and every entry of the table --
+    first and last included -- is read from LDS.  Also the rows' maxima."""
+    from h3_tp2_amd import ops
+    r0, length = 0x6264, 8960                  # the compact table's first rotated key and its length
+    keys = np.arange(r0, r0 + length)
+    bits = ((keys & 1) << 15) | (keys >> 1)    # rotated key -> bf16 bits
+    mag = np.abs(O.bf16_to_f32(bits.astype(np.uint16)))
+    assert mag.min() > 2.5e-9 and mag.max() < 89 and np.isfinite(mag).all()
+    a, w, sa, sb, acc, sa_np, sb_np = _gate_sweep(bits, 96, cuda)
+    amax = torch.zeros(96, device=cuda)
+    h = ops.gemm_swiglu(a, w, sa, sb, row_amax=amax)
+    torch.cuda.synchronize()
+    ref = O.scale_swiglu(acc, sa_np, sb_np)
+    assert np.array_equal(bits16(h), ref)
+    assert torch.equal(amax, h.float().abs().amax(dim=1))
+
+
 def test_ffn_full_size_swiglu_requant_is_the_oracle_of_the_accumulator(cuda):
     """The 1344x768 5 s fused FFN at its full size (M = 31248, gate/up 3072 -> 2 x 8192): the fused gate/up GEMM +
     SwiGLU + requant equals, bit for bit, the oracle's SwiGLU and quant applied to the kernel's own fp32 accumulator
