@@ -22,9 +22,10 @@ verdict book of ``_sites``; compute on kernel 1, the producer kernels and the Sw
   for bit; a site with no bit-identical mode is disabled for the process.
 
 Producer bit identity.  The producer kernels sum the squares exactly (fp64, one rounding to fp32); a stock producer
-that reduces in fp32 rounds some rows' sums differently, and there its bf16 row differs by one ulp (about a third of
-the rows at H = 1024).  A self-check on the first rows cannot see every such row, so ``install`` wires the qkv / fc1
-sites only when the stock producers are this library's own (``own_producers=True``, env
+that reduces in fp32 rounds some rows' sums differently (about 42 % of serving-like rows against torch's CPU fp32
+sum), and on some of those its bf16 row differs by one ulp (1 % of the rows at H = 1024, 3 % at 3072, 4.5 % at 5376;
+the fp8 bytes or scale on 0.07-0.18 %).  A self-check on the first rows cannot see every such row, so
+``install`` wires the qkv / fc1 sites only when the stock producers are this library's own (``own_producers=True``, env
 ``H3_TP2_AMD_OWN_PRODUCERS=1``: the stock ``rms_norm_indexed_scale_shift`` / ``indexed_gate_rms_norm_scale_shift``
 are replaced by the same kernels without the quant, so fused and stock agree by construction -- at the price of
 those one-ulp differences against the upstream producers), or when the caller vouches for the stock producers'
