@@ -871,6 +871,168 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
 }
 
+// ---- the small-M form: at most 32 token rows ----
+// With M <= 32 a GEMM is bound by reading its fp8 weight once (the adaLN modulation: M = 2, 18 432 x 3072 = 56.6 MB),
+// and the 256 x 256 tiles above would spend their k-loop on zero token rows with one tile per 256 weight rows.  Here
+// one wavefront (a workgroup of its own) owns 32 weight rows (one MFMA A block) and all the token rows (one MFMA B
+// block, rows past M read as zeros) and streams its k-steps through a private ring of LDS stages with the LDS-DMA
+// loads of the tiled kernel (whole 128-byte lines, 8 rows per instruction), depth - 1 k-steps ahead of the MFMAs.  A
+// stage holds the 32 weight rows and MB 8-row groups of token rows (MB = 1 for M <= 8, else 4; the lanes of token
+// rows past 8 MB take zero operands), and the ring is as deep as 24 KiB allows (4 stages for MB = 1, 3 for MB = 4),
+// so six waves fit a CU (measured at M = 2, N = 18 432, K = 3072: 24 KiB 11.4 us, 32 KiB 11.7 us, 48 KiB 12.0 us;
+// the k-steps in flight are not what bounds it).  No other wave reads the ring, so no barrier: the wave's own vmcnt wait publishes a stage
+// and its own lgkmcnt wait releases it.
+// Every output element goes through the same MFMA sequence as in gemm_kernel: v_mfma 32x32x64 with the weight row at
+// A-row n % 32 and the token at B-column m % 32, the 64-deep k chunks in ascending order, two per 128-deep k-step (a
+// chunk at or past K reads zeros, as the big tiles' last k-step does), and the same epilogue, so the output is bitwise
+// the big kernel's.
+constexpr int ROWS_MAX_M = 32;
+#ifndef H3_ROWS_RING_KIB
+#define H3_ROWS_RING_KIB 24
+#endif
+constexpr int ROWS_RING_BYTES = H3_ROWS_RING_KIB * 1024;
+
+template <int MB>
+struct RowsRing {
+    static constexpr int STAGE = (32 + 8 * MB) * ROWB;    // 32 weight rows, then 8 MB token rows
+    static constexpr int DEPTH = ROWS_RING_BYTES / STAGE;
+    static constexpr int LOADS = 4 + MB;                  // LDS-DMA instructions per k-step
+    static_assert(DEPTH >= 2 && LOADS * (DEPTH - 1) <= 63, "vmcnt range");
+};
+
+template <int OUT_DT, bool HAS_BIAS, bool AMAX, int MB>
+__global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
+    constexpr int ROWS_DEPTH = RowsRing<MB>::DEPTH;
+    constexpr int ROWS_STAGE = RowsRing<MB>::STAGE;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[ROWS_DEPTH * ROWS_STAGE];
+    const int lane = threadIdx.x;
+    const int r = lane & 31, h = lane >> 5;
+    const int n0 = (int)blockIdx.x * 32;
+    const uint32_t lds0 = lds_addr(lds);
+    const v4u dw = buffer_desc(p.w, p.w_bytes);
+    const v4u da = buffer_desc(p.a, p.a_bytes);
+    // LDS-DMA lane layout (as make_loader): lane l moves row 8 i + (l >> 3) of an 8-row group i, LDS chunk l & 7, which
+    // holds logical chunk (l & 7) ^ swz(row); swz depends on the row's bit 3, so even and odd groups differ
+    const int lrow = lane >> 3;
+    const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz(lrow)), (uint32_t)((lane & 7) ^ swz(lrow + 8))};
+    uint32_t wrow[4], arow[4];                            // byte offsets of this lane's row in each 8-row group
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 8 * i + lrow, m = 8 * i + lrow;
+        wrow[i] = n < p.N ? (uint32_t)((int64_t)n * p.ldw) : OOB;
+        arow[i] = m < p.M ? (uint32_t)((int64_t)m * p.lda) : OOB;
+    }
+    const int nk = (p.K + BK - 1) / BK;
+    // the 4 + MB loads of k-step ks into ring slot `slot`: pieces at or past K read zeros (K % 16 == 0)
+    auto issue = [&](int slot, int ks) {
+        const uint32_t st = lds0 + (uint32_t)slot * ROWS_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = (uint32_t)ks * BK + 16u * lch[i & 1];
+            const bool in = c < (uint32_t)p.K;
+            dma16(dw, st + (uint32_t)i * 8 * ROWB, in && wrow[i] != OOB ? wrow[i] + c : OOB);
+            if (i < MB) dma16(da, st + 32 * ROWB + (uint32_t)i * 8 * ROWB, in && arow[i] != OOB ? arow[i] + c : OOB);
+        }
+    };
+    auto kstep_mfma = [&](v16f& acc, int slot) {
+        const uint8_t* st = lds + slot * ROWS_STAGE;
+        const v8i a0 = read_frag(st, lane, 0), a1 = read_frag(st, lane, 1);
+        v8i b0 = {0, 0, 0, 0, 0, 0, 0, 0}, b1 = b0;
+        if (MB == 4 || r < 8 * MB) {                    // token rows past 8 MB: zero operands, nothing staged
+            b0 = read_frag(st + 32 * ROWB, lane, 0);
+            b1 = read_frag(st + 32 * ROWB, lane, 1);
+        }
+        wait_lgkm0();                                   // the slot is read: the next issue may refill it
+        acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a0, b0, acc, 0, 0, 0, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a1, b1, acc, 0, 0, 0, 0, 0, 0);
+    };
+
+    v16f acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < ROWS_DEPTH; ++s) issue(s, s);
+    // every k-step issues 4 + MB loads (past the last k-step out of range, touching no memory), so when k-step ks is
+    // consumed exactly the loads of the ROWS_DEPTH - 1 younger k-steps may still be in flight
+    int ks = 0;
+    for (; ks + ROWS_DEPTH <= nk; ks += ROWS_DEPTH) {
+#pragma unroll
+        for (int s = 0; s < ROWS_DEPTH; ++s) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(RowsRing<MB>::LOADS * (ROWS_DEPTH - 1)));
+            asm volatile("" ::: "memory");
+            kstep_mfma(acc, s);
+            issue(s, ks + s + ROWS_DEPTH);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < ROWS_DEPTH - 1; ++s) {          // the last nk mod ROWS_DEPTH k-steps, already in flight
+        if (ks + s < nk) {
+            wait_vm0();
+            asm volatile("" ::: "memory");
+            kstep_mfma(acc, s);
+        }
+    }
+    wait_vm0();                                         // the out-of-range tail loads have landed before the exit
+
+    // epilogue: register 4q + rr holds weight row n0 + 8q + 4h + rr for token r (the MFMA result layout)
+    const int m = r;
+    const bool mok = m < p.M;
+    const float sam = mok ? p.sa[(int64_t)m * p.sa_stride] : 0.f;
+    uint32_t rmax = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int n = n0 + 8 * q + 4 * h;               // N % 16 == 0: a group of four is wholly in or out
+        if (!mok || n >= p.N) continue;
+        if (OUT_DT == H3FP8_DT_F32) {
+            const v4f v = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+            *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.y) + (int64_t)m * p.ldy + n) = v;
+            continue;
+        }
+        float v[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float t = p.sb[(int64_t)(n + rr) * p.sb_stride] * acc[4 * q + rr];
+            v[rr] = HAS_BIAS ? __builtin_fmaf(sam, t, load_bias(p.bias, n + rr, OUT_DT)) : sam * t;
+        }
+        uint32_t lo, hi2;
+        if (OUT_DT) {
+            lo = fp16_rne(v[0]) | (fp16_rne(v[1]) << 16);
+            hi2 = fp16_rne(v[2]) | (fp16_rne(v[3]) << 16);
+        } else {
+            lo = cvt_bf16x2(v[0], v[1]);
+            hi2 = cvt_bf16x2(v[2], v[3]);
+        }
+        if (AMAX)
+            rmax = OUT_DT ? max_abs_f16x2(max_abs_f16x2(rmax, lo), hi2) : max_abs_bf16x2(max_abs_bf16x2(rmax, lo), hi2);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * p.ldy + n) = make_uint2(lo, hi2);
+    }
+    if (AMAX) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)rmax, 32, 64);
+        rmax = rmax > o ? rmax : o;
+        if (h == 0 && mok && rmax) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, rmax);
+    }
+}
+
+template <int OUT_DT, bool HAS_BIAS, bool AMAX>
+int launch_rows_t(const GemmParams& p, hipStream_t st) {
+    const dim3 grid((unsigned)((p.N + 31) / 32));
+    if (p.M <= 8) hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 1>), grid, dim3(64), 0, st, p);
+    else hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 4>), grid, dim3(64), 0, st, p);
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+int launch_rows(const GemmParams& p, int epi, int out_dt, bool has_bias, hipStream_t st) {
+    const bool amax = epi == EPI_AMAX;
+    if (out_dt == H3FP8_DT_F32) return launch_rows_t<H3FP8_DT_F32, false, false>(p, st);
+    if (out_dt == H3FP8_DT_BF16) {
+        if (amax) return has_bias ? launch_rows_t<0, true, true>(p, st) : launch_rows_t<0, false, true>(p, st);
+        return has_bias ? launch_rows_t<0, true, false>(p, st) : launch_rows_t<0, false, false>(p, st);
+    }
+    if (amax) return has_bias ? launch_rows_t<1, true, true>(p, st) : launch_rows_t<1, false, true>(p, st);
+    return has_bias ? launch_rows_t<1, true, false>(p, st) : launch_rows_t<1, false, false>(p, st);
+}
+
 __global__ void __launch_bounds__(256) fill_zero_kernel(float* p, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -981,6 +1143,12 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
              int64_t sa_stride, const float* sb, int64_t sb_stride, const void* bias, void* y, int64_t ldy,
              int out_dt, int64_t M, int64_t N, int64_t K, int64_t w_rows, float* row_amax, const uint16_t* silu,
              hipStream_t st) {
+    if (epi != EPI_SWIGLU && M <= ROWS_MAX_M) {
+        // weight-bound: one wave per 32 weight rows (gemm_rows_kernel), bitwise the tiled kernel's output
+        const GemmParams p = make_params(a, lda, w, ldw, sa, sa_stride, sb, sb_stride, bias, y, ldy, M, N, K, w_rows,
+                                         row_amax, silu, false);
+        return launch_rows(p, epi, out_dt, bias != nullptr, st);
+    }
     const int out_elem = (out_dt == H3FP8_DT_F32) ? 4 : 2;
     int64_t rows_per = std::max<int64_t>(BM, ((kMaxBufferBytes - K) / lda + 1) / BM * BM);
     if (sa_stride > 0) rows_per = std::min<int64_t>(rows_per, std::max<int64_t>(BM, kMaxBufferBytes / (4 * sa_stride) / BM * BM));
