@@ -46,6 +46,7 @@ namespace {
 using namespace h3;
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 256;          // tokens per block tile
 constexpr int BN = 256;          // weight rows per block tile
@@ -221,28 +222,27 @@ __device__ __forceinline__ void issue_one(const StageIssue& S, const Loader& L, 
     }
 }
 
-// Weight-tile row of MFMA tile tn (0..3; 0..1 for a half tile) of wave column wn.
-template <int EPI, bool HALF = false>
+// Weight-tile row of MFMA tile tn (0..3) of wave column wn.
+template <int EPI>
 __device__ __forceinline__ int w_tile_row(int wn, int tn) {
-    if (HALF) return wn * 64 + 32 * tn;
     if (EPI == EPI_SWIGLU) return (tn < 2) ? (wn * 64 + 32 * tn) : (128 + wn * 64 + 32 * (tn - 2));
     return wn * 128 + 32 * tn;
 }
 
-template <int EPI, bool HALF = false>
+template <int EPI>
 __device__ __forceinline__ void read_frags(const uint8_t* stage, int wn, int wm, int lane, int sub, v8i af[4],
                                            v8i bf[4]) {
 #pragma unroll
-    for (int t = 0; t < (HALF ? 2 : 4); ++t) af[t] = read_frag(stage + w_tile_row<EPI, HALF>(wn, t) * ROWB, lane, sub);
+    for (int t = 0; t < 4; ++t) af[t] = read_frag(stage + w_tile_row<EPI>(wn, t) * ROWB, lane, sub);
 #pragma unroll
     for (int t = 0; t < 4; ++t) bf[t] = read_frag(stage + A_REGION + (wm * 128 + 32 * t) * ROWB, lane, sub);
 }
 
 // Fragment f of a sub-step: f = 0..3 weight tiles, 4..7 token tiles.
-template <int EPI, bool HALF = false>
+template <int EPI>
 __device__ __forceinline__ void read_one(const uint8_t* stage, int wn, int wm, int lane, int sub, int f, v8i af[4],
                                          v8i bf[4]) {
-    if (f < 4) af[f] = read_frag(stage + w_tile_row<EPI, HALF>(wn, f) * ROWB, lane, sub);
+    if (f < 4) af[f] = read_frag(stage + w_tile_row<EPI>(wn, f) * ROWB, lane, sub);
     else bf[f - 4] = read_frag(stage + A_REGION + (wm * 128 + 32 * (f - 4)) * ROWB, lane, sub);
 }
 
@@ -268,23 +268,19 @@ __device__ __forceinline__ int problem_of(const GroupedParams& gp, int id) {
     return i;
 }
 
-// Global tile id -> problem and tile coordinates.  A half-tile launch covers the full tiles half_first, ... of the
-// full-tile order, two half tiles (256 tokens x 128 channels, tn counted in 128-channel units) per full tile.
-template <bool GROUPED, bool HALF = false>
+// Global tile id -> problem and tile coordinates.
+template <bool GROUPED>
 __device__ __forceinline__ int locate(const GroupedParams& gp, int id, int& tm, int& tn) {
     const int pi = problem_of<GROUPED>(gp, id);
     const GemmParams& p = gp.g[pi];
-    const int local = id - p.tile_offset;
-    tile_of(HALF ? p.half_first + (local >> 1) : local, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.group_m, tm,
-            tn);
-    if (HALF) tn = 2 * tn + (local & 1);
+    tile_of(id - p.tile_offset, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
     return pi;
 }
 
 // Addressing of tile (tm, tn) of problem p for this wave.
 // lane l of an instruction covers row (l >> 3) of an 8-row group and LDS chunk (l & 7), i.e. logical chunk
 // (l & 7) ^ swz(row); swz depends on the row's bits 0..3, so even and odd groups of 8 rows differ.
-template <int EPI, bool HALF = false>
+template <int EPI>
 __device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn, int wave, int lane, Loader& L) {
     const uint32_t lrow = (uint32_t)(lane >> 3);
     const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz((int)lrow)), (uint32_t)((lane & 7) ^ swz((int)lrow + 8))};
@@ -294,11 +290,6 @@ __device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn,
         const int f0 = tn * (BN / 2);
         wrow0 = (wave < 2) ? (int64_t)f0 + 64 * wave : (int64_t)p.N + f0 + 64 * (wave - 2);
         wlimit = (wave < 2) ? (int64_t)p.N : 2 * (int64_t)p.N;
-    } else if (HALF) {
-        // a half tile's 128 weight rows are the shares of waves 0 and 1; waves 2 and 3 load nothing (their share of
-        // the stage is zero-filled and never read)
-        wlimit = p.N;
-        wrow0 = (wave < 2) ? (int64_t)tn * (BN / 2) + 64 * wave : wlimit;
     } else {
         wrow0 = (int64_t)tn * BN + 64 * wave;
         wlimit = p.N;
@@ -342,7 +333,7 @@ struct Cursor {
     uint32_t dsa, dsb;  // LDS addresses of this wave's share of the tile's scale set (set c % NSCALE)
 };
 
-template <int EPI, bool GROUPED, bool HALF = false>
+template <int EPI, bool GROUPED>
 __device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, int c, uint32_t lds0, int wave,
                                            int lane) {
     const int id = (int)blockIdx.x + c * (int)gridDim.x;
@@ -360,10 +351,10 @@ __device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, i
         return;
     }
     int tm, tn;
-    const int pi = locate<GROUPED, HALF>(gp, id, tm, tn);
+    const int pi = locate<GROUPED>(gp, id, tm, tn);
     const GemmParams& p = gp.g[pi];
     I.nk = (p.K + BK - 1) / BK;
-    make_loader<EPI, HALF>(p, tm, tn, wave, lane, I.L);
+    make_loader<EPI>(p, tm, tn, wave, lane, I.L);
 }
 
 // The load instructions of the cursor's k-step for this wave (wofs = the wave's 64-row share within a region).
@@ -400,9 +391,9 @@ __device__ __forceinline__ void issue_scales(uint32_t lds0, const Cursor& I) {
     dma4(I.L.rsb, real ? I.dsb : lds0 + Lds<EPI>::JUNK_OFF + 256, real ? I.L.sb_off : OOB);
 }
 
-template <int EPI, bool GROUPED, bool HALF = false>
+template <int EPI, bool GROUPED>
 __device__ __forceinline__ void cursor_next(Cursor& I, const GroupedParams& gp, uint32_t lds0, int wave, int lane) {
-    if (++I.ks == I.nk) cursor_set<EPI, GROUPED, HALF>(I, gp, I.c + 1, lds0, wave, lane);
+    if (++I.ks == I.nk) cursor_set<EPI, GROUPED>(I, gp, I.c + 1, lds0, wave, lane);
 }
 
 // One k-step g (stage g & 1 holds it, its sub-step-0 fragments are in fa0/fb0, the loads of k-step g+1 are in flight;
@@ -462,54 +453,6 @@ __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const 
     }
 }
 
-// The k-step of a half tile (256 tokens x 128 channels; each wave 128 tokens x 64 channels = 2 x 4 MFMA tiles): the
-// same stage, loads and barriers as kstep, over 16 MFMAs -- u < 8 sub-step 0, u >= 8 sub-step 1:
-//   u < 6        the 6 sub-step-1 fragment reads (2 weight, 4 token tiles);
-//   u == 6       lgkmcnt(0) + barrier 1: the stage is free;
-//   6 < u < 14   the 16 load instructions of k-step g+2 and the two scale loads, three per MFMA;
-//   u == 14      vmcnt + barrier 2: k-step g+1 has landed;
-//   u >= 14      the 6 sub-step-0 fragment reads of k-step g+1.
-constexpr int HALF_REL = 6;
-constexpr int HALF_PUB = 14;
-constexpr int HALF_READ[6] = {0, 1, 4, 5, 6, 7};
-constexpr int HALF_NEXT_READ[6] = {0, 4, 5, 6, 7, 1};
-
-template <int EPI, bool READ_NEXT>
-__device__ __forceinline__ void kstep_half(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, uint32_t wofs, int wn,
-                                           int wm, int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4],
-                                           v8i fb1[4]) {
-    uint8_t* cur = lds + (g & 1) * STAGE_BYTES;
-    uint8_t* nxt = lds + ((g + 1) & 1) * STAGE_BYTES;
-    const StageIssue S = stage_issue<EPI>(lds0 + (uint32_t)(g & 1) * STAGE_BYTES, I, wofs);
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        if (u < 8) mfma_one(acc, fa0, fb0, u);
-        else mfma_one(acc, fa1, fb1, u - 8);
-        if (u < 6) read_one<EPI, true>(cur, wn, wm, lane, 1, HALF_READ[u], fa1, fb1);
-        if (u == HALF_REL) {
-            wait_lgkm0();
-            barrier_nofence();
-        }
-        if (u > HALF_REL && u < HALF_PUB) {
-#pragma unroll
-            for (int k = 3 * (u - HALF_REL - 1); k < 3 * (u - HALF_REL); ++k) {
-                if (k < 16) issue_one<EPI>(S, I.L, k);
-                else if (k == 16) issue_scales<EPI>(lds0, I);
-            }
-        }
-        if (u == HALF_PUB) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(18));  // k-step g+1 (and older) has landed
-            barrier_nofence();
-        }
-        if (READ_NEXT && u >= HALF_PUB) {
-#pragma unroll
-            for (int f = 3 * (u - HALF_PUB); f < 3 * (u - HALF_PUB) + 3; ++f)
-                read_one<EPI, true>(nxt, wn, wm, lane, 0, HALF_NEXT_READ[f], fa0, fb0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
 // Orders one wave's LDS accesses across its lanes: a lane's staging writes become visible to the other lanes' reads
 // that follow.  The wave's LDS accesses already complete in order, so this emits no wait; it is there for the compiler,
 // which under per-lane semantics may otherwise reorder or tail-duplicate lane-divergent writes past other lanes' reads
@@ -547,12 +490,12 @@ __device__ __forceinline__ float zero_to_pos(float x) {
 // 8q + 4(l >> 5) + r of the MFMA tile and token l & 31.  The scaled, rounded outputs go through the wave's staging
 // area, 32 tokens x 64 channels at a time, so that global stores are 16-byte pieces of 128-byte row segments.
 // Scales come from the tile's scale set in LDS (loaded with the tile's first k-step).
-template <int OUT_DT, bool HAS_BIAS, int EPI, bool HALF = false>
+template <int OUT_DT, bool HAS_BIAS, int EPI>
 __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, uint8_t* lds, int set, int wave, int wn,
                                          int wm, int lane, v16f acc[4][4]) {
-    constexpr int NI = HALF ? 2 : 4;                    // MFMA tiles along the channels per wave
-    const int wcol = HALF ? tn * (BN / 2) + wn * 64 : tn * BN + wn * 128;   // the wave's first output channel
-    const int wsb = HALF ? wn * 64 : wn * 128;          // ... and its first entry in the tile's sb set
+    constexpr int NI = 4;                               // MFMA tiles along the channels per wave
+    const int wcol = tn * BN + wn * 128;                // the wave's first output channel
+    const int wsb = wn * 128;                           // ... and its first entry in the tile's sb set
     const int hi = lane >> 5;
     const int mj = lane & 31;
     const int mrow0 = tm * BM + wm * 128;               // first token row of the wave
@@ -799,7 +742,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
 // Persistent kernel: workgroup b computes tiles b, b + G, b + 2G, ... (G = gridDim.x <= the CU count, one workgroup per
 // CU).  The load cursor runs two k-steps ahead of the MFMAs across tile boundaries, so the first two stages of the
 // next tile (and its scales) load while the current tile's last k-steps and epilogue run.
-template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED, bool HALF = false>
+template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED>
 __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[Lds<EPI>::TOTAL];
 
@@ -812,7 +755,7 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     Cursor I;
     const uint32_t lds0 = lds_addr(lds);
     const uint32_t wofs = (uint32_t)wave * 64u * ROWB;  // the wave's 64-row share of a stage region
-    cursor_set<EPI, GROUPED, HALF>(I, gp, 0, lds0, wave, lane);
+    cursor_set<EPI, GROUPED>(I, gp, 0, lds0, wave, lane);
     if (!I.valid) return;
 
     // prologue: k-steps 0 and 1 (and the scales of their tiles) in flight, the sub-step-0 fragments of k-step 0 in
@@ -827,46 +770,44 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
     }
     issue_stage<EPI>(lds0, I, wofs);
     issue_scales<EPI>(lds0, I);
-    cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
+    cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
     issue_stage<EPI>(lds0 + STAGE_BYTES, I, wofs);
     issue_scales<EPI>(lds0, I);
-    if (I.valid) cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
+    if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(18));
     barrier_nofence();
-    read_frags<EPI, HALF>(lds, wn, wm, lane, 0, fa0, fb0);
+    read_frags<EPI>(lds, wn, wm, lane, 0, fa0, fb0);
 
     int g = 0;
     for (int c = 0;; ++c) {
         const int id = (int)blockIdx.x + c * G;
         int tm, tn;
-        const int pi = locate<GROUPED, HALF>(gp, id, tm, tn);
+        const int pi = locate<GROUPED>(gp, id, tm, tn);
         const GemmParams& p = gp.g[pi];
         const int nk = (p.K + BK - 1) / BK;
 
-        v16f acc[4][4];                                 // a half tile uses acc[0..1][*]
+        v16f acc[4][4];
 #pragma unroll
-        for (int i = 0; i < (HALF ? 2 : 4); ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
         for (int ks = 0; ks < nk - 1; ++ks, ++g) {
-            if (HALF) kstep_half<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-            else kstep<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-            if (I.valid) cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
+            kstep<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+            if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
         }
         // the tile's last k-step publishes the next k-step's stage but leaves its fragment registers free for the
         // epilogue; they are read after it
-        if (HALF) kstep_half<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-        else kstep<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
-        if (I.valid) cursor_next<EPI, GROUPED, HALF>(I, gp, lds0, wave, lane);
+        kstep<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
         ++g;
-        epilogue<OUT_DT, HAS_BIAS, EPI, HALF>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
+        epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
         // the next tile's fragment reads stay after the epilogue: hoisted into it they would hold 64 VGPRs across it
         __builtin_amdgcn_sched_barrier(0);
         if (id + G >= gp.total_tiles) break;
-        read_frags<EPI, HALF>(lds + (g & 1) * STAGE_BYTES, wn, wm, lane, 0, fa0, fb0);
+        read_frags<EPI>(lds + (g & 1) * STAGE_BYTES, wn, wm, lane, 0, fa0, fb0);
     }
     wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
 }
@@ -1033,6 +974,308 @@ int launch_rows(const GemmParams& p, int epi, int out_dt, bool has_bias, hipStre
     return has_bias ? launch_rows_t<1, true, false>(p, st) : launch_rows_t<1, false, false>(p, st);
 }
 
+// ---- half tiles (256 tokens x 128 channels) with three stages ----
+// The half-tile form runs a problem's last partial round and whole small problems (a 2048 x 3072 x 3072 linear is 96
+// full tiles, i.e. 192 half tiles on 192 CUs).  A half tile's k-step has half the MFMAs of a full one, and with two
+// stages its loads get about 1.25 k-steps to arrive: it waits on memory latency (about 1.1 us per k-step against
+// 0.55 us of MFMAs).  Its stage is 48 KiB (128 weight rows, then 256 token rows), so three fit the LDS when the
+// epilogue stores from registers instead of staging its tile: the loads of k-step g+3 go out during k-step g, one
+// barrier per k-step both frees stage g and publishes stage g+1, and the loads get about 1.9 k-steps.
+// Every output element goes through the same MFMA sequence and epilogue arithmetic as in the full tiles (weight row at
+// A-row n % 32, token at B-column m % 32, k ascending), so the output is bitwise the full-tile kernel's.
+// Each wave loads 32 weight rows and 64 token rows per k-step (12 LDS-DMA instructions) plus the two scale loads.
+constexpr int H3S_STAGE = (128 + 256) * ROWB;       // 48 KiB
+constexpr int H3S_A = 128 * ROWB;                   // token rows start after the 128 weight rows
+constexpr int H3S_NSTAGE = 3;
+constexpr int H3S_NSCALE = 4;                       // the cursor runs up to 3 tiles ahead (1 k-step per tile)
+constexpr int H3S_SCALES_OFF = H3S_NSTAGE * H3S_STAGE;
+constexpr int H3S_JUNK_OFF = H3S_SCALES_OFF + H3S_NSCALE * SCALE_SET;
+constexpr int H3S_LDS = H3S_JUNK_OFF + 512;
+static_assert(H3S_LDS <= 160 * 1024, "LDS of one CU");
+constexpr int H3S_LOADS = 14;                       // per wave and k-step: 4 weight + 8 token + 2 scale loads
+
+// Half-tile launch: workgroup id -> (tile position in the full-tile order, column half).  The full-tile launch before it
+// took workgroups b < full of the XCD-contiguous map over all T full tiles, i.e. the first full / 8 positions of each of
+// the 8 per-XCD ranges; the R = T - full positions left are the tails of those ranges.  They are listed range by range
+// (so consecutive entries are consecutive positions), split in two halves each, and dealt to the half-tile workgroups
+// by the same XCD-contiguous rule: the two halves of a tile and neighbouring tiles run on one XCD and share its L2.
+__device__ __forceinline__ void half_tile_of(const GemmParams& p, int id, int n_half, int& tm, int& tn) {
+    const int xcd = id & 7, local = id >> 3;
+    const int per = n_half >> 3, rem = n_half & 7;
+    const int lid = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    int k = lid >> 1;
+    const int T = p.tiles_m * p.tiles_n, pT = T >> 3, rT = T & 7, done = p.half_first >> 3;
+    int c = 0;
+    for (; c < 7; ++c) {
+        const int n_c = pT + (c < rT ? 1 : 0) - done;
+        if (k < n_c) break;
+        k -= n_c;
+    }
+    const int pos = ((c < rT) ? c * (pT + 1) : rT * (pT + 1) + (c - rT) * pT) + done + k;
+    const int in_group = p.group_m * p.tiles_n;
+    const int g = pos / in_group;
+    const int first = g * p.group_m;
+    const int gsz = min(p.tiles_m - first, p.group_m);
+    const int r = pos - g * in_group;
+    tm = first + r % gsz;
+    tn = 2 * (r / gsz) + (lid & 1);
+}
+
+struct Half3Cursor {
+    v4u rw, ra, rsa, rsb;
+    uint32_t vw[2], va[2], vw_t[2], va_t[2];        // lane parts (even / odd 8-row groups); _t: the K-tail k-step
+    uint32_t row8_w, row8_a;
+    uint32_t sa_off, sb_off;
+    uint32_t dsa, dsb;                              // this wave's share of the tile's scale set (junk when unused)
+    int c, ks, nk;
+    bool valid;
+};
+
+__device__ __forceinline__ void h3s_cursor_set(Half3Cursor& I, const GroupedParams& gp, int c, uint32_t lds0,
+                                               int wave, int lane) {
+    const int id = (int)blockIdx.x + c * (int)gridDim.x;
+    I.c = c;
+    I.ks = 0;
+    I.valid = id < gp.total_tiles;
+    const uint32_t set = lds0 + H3S_SCALES_OFF + (uint32_t)(c % H3S_NSCALE) * SCALE_SET;
+    I.dsa = set + 256u * (uint32_t)wave;
+    I.dsb = wave < 2 ? set + 1024u + 256u * (uint32_t)wave : lds0 + H3S_JUNK_OFF;
+    if (!I.valid) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) I.vw[e] = I.va[e] = I.vw_t[e] = I.va_t[e] = OOB;
+        I.sa_off = I.sb_off = OOB;
+        I.nk = 1;
+        return;
+    }
+    int tm, tn;
+    const GemmParams& p = gp.g[0];
+    half_tile_of(p, id, gp.total_tiles, tm, tn);
+    I.nk = (p.K + BK - 1) / BK;
+    const uint32_t lrow = (uint32_t)(lane >> 3);
+    const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz((int)lrow)), (uint32_t)((lane & 7) ^ swz((int)lrow + 8))};
+    const int64_t wrow0 = (int64_t)tn * (BN / 2) + 32 * wave;    // this wave's 32 weight rows
+    const int64_t arow0 = (int64_t)tm * BM + 64 * wave;          // ... and 64 token rows
+    I.rw = buffer_desc(p.w, p.w_bytes);
+    I.ra = buffer_desc(p.a, p.a_bytes);
+    const uint32_t ktail = (uint32_t)(p.K % BK);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t c16 = 16u * lch[e];
+        I.vw[e] = (wrow0 >= p.N) ? OOB : (uint32_t)((wrow0 + lrow) * p.ldw) + c16;   // rows past N: past the range
+        I.va[e] = (arow0 >= p.M) ? OOB : (uint32_t)((arow0 + lrow) * p.lda) + c16;   // rows past M: past the range
+        const bool cut = ktail != 0 && c16 >= ktail;
+        I.vw_t[e] = cut ? OOB : I.vw[e];
+        I.va_t[e] = cut ? OOB : I.va[e];
+    }
+    I.row8_w = (uint32_t)(8 * p.ldw);
+    I.row8_a = (uint32_t)(8 * p.lda);
+    I.rsa = buffer_desc(p.sa, p.sa_stride ? (uint32_t)((p.M - 1) * p.sa_stride * 4 + 4) : 4u);
+    I.rsb = buffer_desc(p.sb, p.sb_stride ? (uint32_t)((p.w_rows - 1) * p.sb_stride * 4 + 4) : 4u);
+    const int64_t srow = arow0 + lane;                            // sa of token row 64 wave + lane
+    I.sa_off = (srow < p.M) ? (uint32_t)(srow * p.sa_stride * 4) : OOB;
+    const int64_t wr = (int64_t)tn * (BN / 2) + 64 * wave + lane;  // waves 0, 1: sb of the tile's 128 weight rows
+    I.sb_off = (wave < 2 && wr < p.N) ? (uint32_t)(wr * p.sb_stride * 4) : OOB;
+}
+
+__device__ __forceinline__ void h3s_cursor_next(Half3Cursor& I, const GroupedParams& gp, uint32_t lds0, int wave,
+                                                int lane) {
+    if (++I.ks == I.nk) h3s_cursor_set(I, gp, I.c + 1, lds0, wave, lane);
+}
+
+// Load j (0..13) of the cursor's k-step into stage `st`: 0..3 the wave's weight rows (8 per instruction), 4..11 its
+// token rows, 12 / 13 the scales (into the tile's scale set at its first k-step, else into the scratch slot).
+__device__ __forceinline__ void h3s_issue_one(const Half3Cursor& I, uint32_t st, uint32_t lds0, int wave, int j) {
+    const bool last = I.ks == I.nk - 1;
+    const uint32_t k0 = (uint32_t)I.ks * BK;
+    if (j < 4) {
+        const uint32_t off = (last ? I.vw_t[j & 1] : I.vw[j & 1]);
+        dma16(I.rw, st + (uint32_t)(32 * wave + 8 * j) * ROWB, off == OOB ? OOB : off + k0 + (uint32_t)j * I.row8_w);
+    } else if (j < 12) {
+        const int i = j - 4;
+        const uint32_t off = (last ? I.va_t[i & 1] : I.va[i & 1]);
+        dma16(I.ra, st + H3S_A + (uint32_t)(64 * wave + 8 * i) * ROWB,
+              off == OOB ? OOB : off + k0 + (uint32_t)i * I.row8_a);
+    } else {
+        const bool real = I.valid && I.ks == 0;
+        if (j == 12) dma4(I.rsa, real ? I.dsa : lds0 + H3S_JUNK_OFF, real ? I.sa_off : OOB);
+        else dma4(I.rsb, real ? I.dsb : lds0 + H3S_JUNK_OFF, real ? I.sb_off : OOB);
+    }
+}
+
+// Fragment f of a sub-step (0, 1: the wave's two 32-row weight tiles; 2..5: its four 32-row token tiles).
+__device__ __forceinline__ void h3s_read(const uint8_t* stage, int wn, int wm, int lane, int sub, int f, v8i af[4],
+                                         v8i bf[4]) {
+    if (f < 2) af[f] = read_frag(stage + (wn * 64 + 32 * f) * ROWB, lane, sub);
+    else bf[f - 2] = read_frag(stage + H3S_A + (wm * 128 + 32 * (f - 2)) * ROWB, lane, sub);
+}
+
+// One k-step over 16 MFMA slots (u < 8 sub-step 0, u >= 8 sub-step 1):
+//   u < 6       the 6 sub-step-1 fragment reads of stage g;
+//   u == 7      lgkmcnt(0) + vmcnt(14) + barrier: every wave's reads of stage g have returned (it is free) and k-step
+//               g+1 has landed (only the loads of k-step g+2 may still be in flight);
+//   8 <= u < 15 the 14 loads of k-step g+3 into stage g, two per MFMA;
+//   8 <= u < 14 the 6 sub-step-0 fragment reads of k-step g+1.
+template <bool READ_NEXT>
+__device__ __forceinline__ void h3s_kstep(uint8_t* lds, uint32_t lds0, int s0, const Half3Cursor& I, int wave, int wn,
+                                          int wm, int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4],
+                                          v8i fb1[4]) {
+    const int s1 = s0 == H3S_NSTAGE - 1 ? 0 : s0 + 1;
+    const uint8_t* cur = lds + s0 * H3S_STAGE;
+    const uint8_t* nxt = lds + s1 * H3S_STAGE;
+    const uint32_t st = lds0 + (uint32_t)s0 * H3S_STAGE;
+    constexpr int NEXT_ORDER[6] = {0, 2, 3, 4, 5, 1};   // weight tile 0 and the token tiles first: MFMA t uses
+                                                        // weight tile t / 4 and token tile t % 4
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        if (u < 8) mfma_one(acc, fa0, fb0, u);
+        else mfma_one(acc, fa1, fb1, u - 8);
+        if (u < 6) h3s_read(cur, wn, wm, lane, 1, u, fa1, fb1);
+        if (u == 7) {
+            wait_lgkm0();
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(H3S_LOADS));
+            barrier_nofence();
+        }
+        if (u >= 8 && u < 15) {
+            h3s_issue_one(I, st, lds0, wave, 2 * (u - 8));
+            h3s_issue_one(I, st, lds0, wave, 2 * (u - 8) + 1);
+        }
+        if (READ_NEXT && u >= 8 && u < 14) h3s_read(nxt, wn, wm, lane, 0, NEXT_ORDER[u - 8], fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Epilogue of a half tile straight from the accumulators (no LDS staging): register 4q + r of MFMA tile (i, j) is
+// channel col0 + 32 i + 8 q + 4 (lane >> 5) + r of token mrow0 + 32 j + (lane & 31); each lane stores its 4
+// consecutive channels (8 bytes, 16 contiguous bytes with the partner lane l ^ 32).  Rows past M fall outside the
+// output descriptor's range, columns past N get an out-of-range offset.
+template <int OUT_DT, bool HAS_BIAS, int EPI>
+__device__ __forceinline__ void h3s_epilogue(const GemmParams& p, int tm, int tn, const uint8_t* lds, int set, int wn,
+                                             int wm, int lane, v16f acc[4][4]) {
+    const int hi = lane >> 5, mj = lane & 31;
+    const int col0 = tn * (BN / 2) + wn * 64;
+    const int mrow0 = tm * BM + wm * 128;
+    const float* sa_l = reinterpret_cast<const float*>(lds + H3S_SCALES_OFF + set * SCALE_SET);
+    const float* sb_l = sa_l + 256;
+    if (OUT_DT == H3FP8_DT_F32) {
+        float* yf = reinterpret_cast<float*>(p.y);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = col0 + 32 * i + 8 * q + 4 * hi;
+                    const int m = mrow0 + 32 * j + mj;
+                    if (n < p.N && m < p.M) {
+                        const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                       acc[i][j][4 * q + 3]};
+                        *reinterpret_cast<v4f*>(yf + (int64_t)m * p.ldy + n) = v;
+                    }
+                }
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(p.y, p.y_bytes);
+    const uint32_t row2 = (uint32_t)p.ldy * 2u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = mrow0 + 32 * j + mj;
+        const float sam = sa_l[wm * 128 + 32 * j + mj];
+        uint32_t rmax = 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = col0 + 32 * i + 8 * q + 4 * hi;
+                const v4f sbn = *reinterpret_cast<const v4f*>(sb_l + wn * 64 + 32 * i + 8 * q + 4 * hi);
+                float bn[4] = {0, 0, 0, 0};
+                if (HAS_BIAS) {
+                    const int nc = n < p.N ? n : 0;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) bn[r] = load_bias(p.bias, nc + r, OUT_DT);
+                }
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float t = sbn[r] * acc[i][j][4 * q + r];
+                    v[r] = HAS_BIAS ? __builtin_fmaf(sam, t, bn[r]) : sam * t;
+                }
+                uint32_t lo, hi2;
+                if (OUT_DT) {
+                    lo = fp16_rne(v[0]) | (fp16_rne(v[1]) << 16);
+                    hi2 = fp16_rne(v[2]) | (fp16_rne(v[3]) << 16);
+                } else {
+                    lo = cvt_bf16x2(v[0], v[1]);
+                    hi2 = cvt_bf16x2(v[2], v[3]);
+                }
+                if (EPI == EPI_AMAX && n < p.N && m < p.M)
+                    rmax = OUT_DT ? max_abs_f16x2(max_abs_f16x2(rmax, lo), hi2)
+                                  : max_abs_bf16x2(max_abs_bf16x2(rmax, lo), hi2);
+                const uint32_t off = (n < p.N) ? (uint32_t)m * row2 + (uint32_t)n * 2u : OOB;
+                const v2u32 val = {lo, hi2};
+                __builtin_amdgcn_raw_buffer_store_b64(val, yr, off, 0, 0);
+            }
+        if (EPI == EPI_AMAX) {
+            const uint32_t o = (uint32_t)__shfl_xor((int)rmax, 32, 64);
+            rmax = rmax > o ? rmax : o;
+            if (hi == 0 && m < p.M && rmax) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, rmax);
+        }
+    }
+}
+
+template <int OUT_DT, bool HAS_BIAS, int EPI>
+__global__ void __launch_bounds__(256, 1) gemm_half3_kernel(GroupedParams gp) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[H3S_LDS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wn = wave & 1, wm = wave >> 1;
+    const int G = (int)gridDim.x;
+    const uint32_t lds0 = lds_addr(lds);
+    Half3Cursor I;
+    h3s_cursor_set(I, gp, 0, lds0, wave, lane);
+    if (!I.valid) return;
+    // prologue: k-steps 0, 1, 2 in flight (14 loads each), then stage 0 published
+#pragma unroll
+    for (int s = 0; s < H3S_NSTAGE; ++s) {
+#pragma unroll
+        for (int j = 0; j < H3S_LOADS; ++j) h3s_issue_one(I, lds0 + (uint32_t)s * H3S_STAGE, lds0, wave, j);
+        if (I.valid) h3s_cursor_next(I, gp, lds0, wave, lane);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * H3S_LOADS));
+    barrier_nofence();
+    v8i fa0[4], fb0[4], fa1[4], fb1[4];
+#pragma unroll
+    for (int f = 0; f < 6; ++f) h3s_read(lds, wn, wm, lane, 0, f, fa0, fb0);
+    int s0 = 0;
+    for (int c = 0;; ++c) {
+        const int id = (int)blockIdx.x + c * G;
+        int tm, tn;
+        const GemmParams& p = gp.g[0];
+        half_tile_of(p, id, gp.total_tiles, tm, tn);
+        const int nk = (p.K + BK - 1) / BK;
+        v16f acc[4][4];                                 // acc[0..1][*] used
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int ks = 0; ks < nk - 1; ++ks) {
+            h3s_kstep<true>(lds, lds0, s0, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+            if (I.valid) h3s_cursor_next(I, gp, lds0, wave, lane);
+            s0 = s0 == H3S_NSTAGE - 1 ? 0 : s0 + 1;
+        }
+        h3s_kstep<false>(lds, lds0, s0, I, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        if (I.valid) h3s_cursor_next(I, gp, lds0, wave, lane);
+        s0 = s0 == H3S_NSTAGE - 1 ? 0 : s0 + 1;
+        h3s_epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % H3S_NSCALE, wn, wm, lane, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (id + G >= gp.total_tiles) break;
+#pragma unroll
+        for (int f = 0; f < 6; ++f) h3s_read(lds + s0 * H3S_STAGE, wn, wm, lane, 0, f, fa0, fb0);
+    }
+    wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
+}
+
 __global__ void __launch_bounds__(256) fill_zero_kernel(float* p, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -1048,21 +1291,40 @@ int zero_rows(float* p, int64_t n, hipStream_t st) {
 // Workgroups of a persistent launch over `tiles` tiles: one per CU, at most one per tile.
 int grid_for(int tiles) { return std::max(1, std::min(tiles, h3host::cu_count())); }
 
-template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED, bool HALF = false>
+template <int OUT_DT, bool HAS_BIAS, int EPI, bool GROUPED>
 int launch_one(const GroupedParams& gp, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI, GROUPED, HALF>), dim3(grid_for(gp.total_tiles)), dim3(256), 0,
-                       st, gp);
+    hipLaunchKernelGGL((gemm_kernel<OUT_DT, HAS_BIAS, EPI, GROUPED>), dim3(grid_for(gp.total_tiles)), dim3(256), 0, st,
+                       gp);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
 
-template <int EPI, bool HALF = false>
+template <int EPI>
 int dispatch(const GroupedParams& gp, int out_dt, bool has_bias, hipStream_t st) {
     if (out_dt == H3FP8_DT_BF16) {
-        return has_bias ? launch_one<0, true, EPI, false, HALF>(gp, st) : launch_one<0, false, EPI, false, HALF>(gp, st);
+        return has_bias ? launch_one<0, true, EPI, false>(gp, st) : launch_one<0, false, EPI, false>(gp, st);
     }
-    if (out_dt == H3FP8_DT_F32) return launch_one<H3FP8_DT_F32, false, EPI_PLAIN, false, HALF>(gp, st);
-    return has_bias ? launch_one<1, true, EPI, false, HALF>(gp, st) : launch_one<1, false, EPI, false, HALF>(gp, st);
+    if (out_dt == H3FP8_DT_F32) return launch_one<H3FP8_DT_F32, false, EPI_PLAIN, false>(gp, st);
+    return has_bias ? launch_one<1, true, EPI, false>(gp, st) : launch_one<1, false, EPI, false>(gp, st);
+}
+
+template <int OUT_DT, bool HAS_BIAS, int EPI>
+int launch_half3(const GroupedParams& gp, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_half3_kernel<OUT_DT, HAS_BIAS, EPI>), dim3(grid_for(gp.total_tiles)), dim3(256), 0, st, gp);
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+int dispatch_half3(const GroupedParams& gp, int epi, int out_dt, bool has_bias, hipStream_t st) {
+    if (out_dt == H3FP8_DT_F32) return launch_half3<H3FP8_DT_F32, false, EPI_PLAIN>(gp, st);
+    if (epi == EPI_AMAX) {
+        if (out_dt == H3FP8_DT_BF16)
+            return has_bias ? launch_half3<0, true, EPI_AMAX>(gp, st) : launch_half3<0, false, EPI_AMAX>(gp, st);
+        return has_bias ? launch_half3<1, true, EPI_AMAX>(gp, st) : launch_half3<1, false, EPI_AMAX>(gp, st);
+    }
+    if (out_dt == H3FP8_DT_BF16)
+        return has_bias ? launch_half3<0, true, EPI_PLAIN>(gp, st) : launch_half3<0, false, EPI_PLAIN>(gp, st);
+    return has_bias ? launch_half3<1, true, EPI_PLAIN>(gp, st) : launch_half3<1, false, EPI_PLAIN>(gp, st);
 }
 
 // The last, partial round of a launch with full tiles leaves most CUs idle.  When its tiles fit one round as half
@@ -1087,8 +1349,7 @@ int launch_split(GroupedParams gp, int epi, int out_dt, bool has_bias, hipStream
     }
     gp.g[0].half_first = full_tiles;
     gp.total_tiles = 2 * rest;
-    if (epi == EPI_PLAIN) return dispatch<EPI_PLAIN, true>(gp, out_dt, has_bias, st);
-    return dispatch<EPI_AMAX, true>(gp, out_dt, has_bias, st);
+    return dispatch_half3(gp, epi, out_dt, has_bias, st);
 }
 
 constexpr int64_t kMaxBufferBytes = 0x7fff0000LL;   // buffer offsets are 32-bit; keep clear of the OOB marker
