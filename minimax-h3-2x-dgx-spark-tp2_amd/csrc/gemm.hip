@@ -1363,6 +1363,8 @@ int check_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const flo
                (long long)N);
     H3_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, "%s: size too large", who);
     if (M == 0 || N == 0) return H3FP8_OK;
+    // an empty reduction is refused rather than run: the k-loops assume at least one k-step
+    H3_REQUIRE(K > 0, "%s: K must be positive (got 0)", who);
     H3_REQUIRE(a && w && sa && sb && y, "%s: null pointer", who);
     H3_REQUIRE(lda >= K && lda % 16 == 0 && ldw >= K && ldw % 16 == 0, "%s: lda/ldw must be >= K and multiples of 16",
                who);

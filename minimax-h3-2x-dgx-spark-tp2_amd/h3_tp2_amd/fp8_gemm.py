@@ -58,6 +58,8 @@ def eligible(a, b, scale_a, scale_b, out_dtype, bias=None) -> bool:  # noqa: ANN
         return False
     if not a.is_contiguous() or not b.t().is_contiguous() or a.shape[1] % 16 or N % 16:
         return False
+    if a.shape[1] == 0:                                        # an empty reduction: the stock op (the kernels refuse it)
+        return False
     return True
 
 

@@ -41,6 +41,8 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
     assert rc == -22 and b"multiple of 8" in L.h3fp8_last_error()
     rc = L.h3fp8_gemm(None, 32, None, 32, None, 1, None, 1, None, None, 32, 0, 4, 24, 24, None, None)
     assert rc == -22 and b"multiples of 16" in L.h3fp8_last_error()
+    rc = L.h3fp8_gemm(None, 32, None, 32, None, 1, None, 1, None, None, 32, 0, 4, 32, 0, None, None)
+    assert rc == -22 and b"K must be positive" in L.h3fp8_last_error()
 
 
 def test_missing_library_fails_loudly(tmp_path):

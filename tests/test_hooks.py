@@ -71,6 +71,8 @@ def test_eligibility_matches_reference_rules():
     assert not fp8_gemm.eligible(a3, b3, sa3, sb3, BF16)                      # N % 16
     assert not fp8_gemm.eligible(a.unsqueeze(0), b, sa, sb, BF16)
     assert not fp8_gemm.eligible(a, operands(K=80)[1], sa, sb, BF16)          # K mismatch
+    a4, b4, sa4, sb4 = operands(K=0)
+    assert not fp8_gemm.eligible(a4, b4, sa4, sb4, BF16)                      # empty reduction
 
 
 def test_install_routes_eligible_calls_and_keeps_stock(monkeypatch):
