@@ -10,6 +10,7 @@
 """
 from __future__ import annotations
 
+import contextlib
 import logging
 from typing import Any, Callable, Iterable
 
@@ -22,6 +23,36 @@ def site_layer(block, site: str):  # noqa: ANN001,ANN201
     """The linear layer of ``site`` in ``block`` (None when the block has no such layer)."""
     owner, name = SITE_LAYERS[site]
     return getattr(getattr(block, owner, None), name, None)
+
+
+def layer_refusal(site: str, layer, lora_types) -> str | None:  # noqa: ANN001
+    """Why ``site``'s layer cannot carry a block-scoped stash or route (None: it can): it must exist, be the plain
+    layer (not a LoRA wrapper) and hold its whole output (a sharded layer's collective would read the placeholder)."""
+    if layer is None:
+        return f"{site}: the block has no {'.'.join(SITE_LAYERS[site])}"
+    if lora_types and isinstance(layer, lora_types):
+        return f"{site}: the layer sits inside a LoRA wrapper"
+    shards = getattr(layer, "tp_size", 1)
+    if shards != 1:
+        return f"{site}: the layer is split over {shards} ranks (tp_size != 1)"
+    return None
+
+
+@contextlib.contextmanager
+def block_scope(tls, scope):  # noqa: ANN001
+    """``scope`` is the thread's running block scope (``tls.ctx``) while the body runs; the enclosing block's scope
+    comes back afterwards.  A normal exit closes the scope (``scope.close()``: whatever the block left waiting is made
+    real for whoever holds it); an exception drops it (``scope.drop()``) and propagates."""
+    outer = getattr(tls, "ctx", None)
+    tls.ctx = scope
+    try:
+        yield scope
+    except BaseException:
+        tls.ctx = outer
+        scope.drop()
+        raise
+    tls.ctx = outer
+    scope.close()
 
 
 def tracing() -> bool:
@@ -64,7 +95,8 @@ def checked(book: dict, stats: dict, notes: Notes, key: tuple, fused: Callable[[
     try:
         ok = same_bits(fused(), stock())
     except Exception as exc:  # noqa: BLE001  (a fused form that cannot even run is a failed check)
-        notes.logger.warning(notes.prefix + "self-check %s raised %s: %s", key, type(exc).__name__, exc)
+        notes.logger.warning(notes.prefix + "the fused form of %s failed to run (%s: %s)", key, type(exc).__name__,
+                             exc)
         ok = False
     verdicts[key] = ok
     stats["selfcheck_pass" if ok else "selfcheck_fail"] += 1

@@ -63,7 +63,8 @@ def scale_pass_into(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias:
 
 
 class Stash:
-    """The fp32 product of one GEMM and its epilogue operands, kept in place of the scale pass's output ``ph``."""
+    """What the stash hook keeps instead of running the scale pass: the GEMM's raw fp32 product, its per-token and
+    per-channel scales and bias, and ``ph``, the uninitialised bf16 tensor handed to the model in its place."""
     __slots__ = ("x32", "sa", "sb", "bias", "ph")
 
     def __init__(self, x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
@@ -93,7 +94,8 @@ class ConsumerScope:
         for site, st in list(self.pending.items()):
             st.materialize()
             _stats["materialize"] += 1
-            _notes.once("mat-" + reason, "%s: stash of %s materialised, stock consumer", reason, site)
+            _notes.once("mat-" + reason, "%s: the %s output was computed after all (its consumer runs stock)", reason,
+                        site)
         self.pending.clear()
 
     def claim(self, site: str) -> Stash | None:
@@ -103,11 +105,19 @@ class ConsumerScope:
             return None
         st = self.pending.get(site)
         if st is None:
-            self.flush(f"{site} consumer saw another site's stash")
+            self.flush(f"the {site} consumer found a stash of another site")
         return st
 
     def settle(self, site: str) -> None:
         self.pending.pop(site, None)
+
+    def close(self) -> None:
+        """The block returned: a stash nobody consumed is computed for whoever still holds its placeholder."""
+        self.flush("the block returned with its stash unconsumed")
+
+    def drop(self) -> None:
+        """The block raised: nothing will read the placeholders."""
+        self.pending.clear()
 
 
 _Ctx = ConsumerScope          # the name the protocol tests address
@@ -131,7 +141,7 @@ def stash_hook(a, b, scale_a, scale_b, out_dtype, bias):  # noqa: ANN001
     site = scope.want.pop(_sites_key(b), None)
     if site is None:
         return None
-    scope.flush(f"unconsumed stash before {site}")
+    scope.flush(f"a {site} GEMM arrived before the earlier stash was consumed")
     M, N = a.shape[0], b.shape[1]
     ph = torch.empty((M, N), device=a.device, dtype=out_dtype)
     scope.pending[site] = Stash(fp8_gemm.product_fp32(a, b), _vec(scale_a, M), _vec(scale_b, N), bias, ph)
@@ -266,13 +276,13 @@ def qk_mismatch(st: Stash, q, k, q_weight, k_weight, rope_table, head_dim, rotar
 
     return _first_failure((
         ("interleaved", lambda: not interleaved),
-        ("q/k rank or dtype", ranks),
+        ("q / k are not bf16 [T, heads, head_dim]", ranks),
         ("shapes", shapes),
-        ("placeholder/product layout", lambda: ph.is_contiguous() and x32.is_contiguous() and x32.shape == ph.shape),
-        ("q/k are not the split views of the qkv placeholder", views),
+        ("stash not dense", lambda: ph.is_contiguous() and x32.is_contiguous() and x32.shape == ph.shape),
+        ("q / k do not view the stashed qkv output", views),
         ("head_dim", lambda: q.shape[-1] == HEAD_DIM and head_dim in (None, HEAD_DIM)),
         ("rotary", rotary),
-        ("rope table or norm weight dtype/shape", tables),
+        ("norm weights or rope table of another shape or type", tables),
         ("device", lambda: _same_cuda_device(x32, q_weight, k_weight, rope_table)),
     ))
 
@@ -289,12 +299,13 @@ def rows_mismatch(st: Stash, x: torch.Tensor, branch: torch.Tensor, *others: tor
     ph, x32 = st.ph, st.x32
     tables, idx = others[:-1], others[-1]
     return _first_failure((
-        ("branch is not the placeholder", lambda: _is_view_of(branch, ph) and branch.shape == ph.shape),
-        ("residual shape/dtype/layout", lambda: x.dim() == 2 and x.shape == ph.shape and x.dtype == torch.bfloat16
+        ("the branch is not the stashed output", lambda: _is_view_of(branch, ph) and branch.shape == ph.shape),
+        ("the residual is not a dense bf16 twin of it", lambda: x.dim() == 2 and x.shape == ph.shape
+         and x.dtype == torch.bfloat16
          and x.is_contiguous() and ph.is_contiguous() and x32.is_contiguous() and x32.shape == ph.shape),
         ("no rows", lambda: x.shape[0] > 0),
         ("width", lambda: x.shape[1] % 8 == 0 and x.shape[1] <= 8192),
-        ("gate/shift/scale layout", lambda: _row_tables_ok(x.shape[1], tables)),
+        ("modulation tables the kernel cannot index", lambda: _row_tables_ok(x.shape[1], tables)),
         ("indices", lambda: idx.dim() == 1 and idx.shape[0] == x.shape[0] and idx.dtype in (torch.int32, torch.int64)),
         ("device", lambda: _same_cuda_device(x, x32, *others)),
     ))
@@ -404,54 +415,42 @@ FUSED_FACTORIES = {"qkv": make_fused_qk, "out": make_fused_gate_rms, "fc2": make
 
 # ---- the block scope -------------------------------------------------------------------------------------------------
 
-def _layer_refusal(site: str, layer, lora_types) -> str | None:  # noqa: ANN001
-    """Why ``site``'s GEMM cannot be stashed (None: it can)."""
-    if layer is None or (lora_types and isinstance(layer, lora_types)):
-        return f"{site}: missing or LoRA-wrapped layer"
-    if getattr(layer, "tp_size", 1) != 1:
-        return f"{site}: tp_size != 1 (an all-reduce would read the placeholder)"
+def _stashable(site: str, layer, lora_types) -> str | None:  # noqa: ANN001
+    """Why ``site``'s GEMM output cannot be replaced by a stash (None: it can): on top of the shared layer rules, the
+    weight must be the dense FP8 [K, N] matrix the dispatcher sees (no padded output columns)."""
+    why = _sites.layer_refusal(site, layer, lora_types)
+    if why is not None:
+        return why
     w = getattr(layer, "weight", None)
     width = int(getattr(layer, "output_size_per_partition", 0) or 0)
-    if not (isinstance(w, torch.Tensor) and w.dtype == torch.float8_e4m3fn and w.dim() == 2 and w.shape[1] == width):
-        return f"{site}: weight is not an unpadded FP8 [K, N] tensor"
-    return None
+    dense = isinstance(w, torch.Tensor) and w.dtype == torch.float8_e4m3fn and w.dim() == 2 and w.shape[1] == width
+    return None if dense else f"{site}: its weight is not a dense e4m3 [K, {width}] matrix"
 
 
 def block_plan(block, sites, lora_types=()) -> tuple[dict | None, str]:  # noqa: ANN001
-    """{(weight data_ptr, weight shape): site} for this block's eligible GEMMs, or (None, reason)."""
+    """The weights of this block whose GEMMs may be stashed, as {weight key: site}, or (None, why not).  Every site
+    still enabled must qualify, or the block runs stock."""
     if _sites.tracing():
-        return None, "torch.compile tracing"
-    live = [site for site in sites if site not in _state["disabled"]]
-    layers = {site: _sites.site_layer(block, site) for site in live}
-    for site in live:
-        reason = _layer_refusal(site, layers[site], lora_types)
-        if reason is not None:
-            return None, reason
-    want = {_sites_key(layers[site].weight): site for site in live}
-    return (want or None), "no site left"
+        return None, "inside a torch.compile trace"
+    layers = {site: _sites.site_layer(block, site) for site in sites if site not in _state["disabled"]}
+    refusals = [why for why in (_stashable(site, layer, lora_types) for site, layer in layers.items()) if why]
+    if refusals:
+        return None, refusals[0]
+    want = {_sites_key(layer.weight): site for site, layer in layers.items()}
+    return (want or None), "every site is disabled"
 
 
 def make_block_forward(orig_forward, sites, lora_types=()):  # noqa: ANN001,ANN201
-    """Run a DiT block's forward inside a ConsumerScope (thread-local; the enclosing scope comes back afterwards); a
-    stash still waiting when the block returns is materialised."""
+    """Run a DiT block's forward inside a ConsumerScope (``_sites.block_scope``: thread-local, nested blocks restore
+    the outer scope, a stash left waiting at the end is computed after all)."""
     @functools.wraps(orig_forward)
     def forward(self, *args, **kwargs):  # noqa: ANN001,ANN202
-        want, reason = block_plan(self, sites, lora_types)
+        want, why = block_plan(self, sites, lora_types)
         if want is None:
-            _notes.once("plan-" + reason, "block not planned (%s); stock path", reason)
+            _notes.once("plan-" + why, "%s: this block's consumers run stock", why)
             return orig_forward(self, *args, **kwargs)
-        scope, outer = ConsumerScope(want), _scope()
-        _tls.ctx = scope
-        finished = False
-        try:
-            result = orig_forward(self, *args, **kwargs)
-            finished = True
-        finally:
-            _tls.ctx = outer
-            if finished:
-                scope.flush("stash left at the end of the block")
-            scope.pending.clear()
-        return result
+        with _sites.block_scope(_tls, ConsumerScope(want)):
+            return orig_forward(self, *args, **kwargs)
 
     forward._h3_tp2_amd_consumer = True
     return forward

@@ -220,7 +220,7 @@ def install(ops_module=None, level: str = "hip", check: bool = True) -> bool:  #
     False is returned (the reference likewise keeps a working path when a level's probe fails,
     h3_tp2/fp8_gemm.py:387-410).  Level "off" leaves the op alone."""
     if level not in LEVELS:
-        raise ValueError(f"unknown FP8 GEMM level {level!r}")
+        raise ValueError(f"FP8 GEMM level must be one of {sorted(LEVELS)}, got {level!r}")
     if ops_module is None:
         from vllm import _custom_ops as ops_module  # noqa: PLC0415  (the caller passes the module where vLLM is absent)
     orig = ops_module.cutlass_scaled_mm

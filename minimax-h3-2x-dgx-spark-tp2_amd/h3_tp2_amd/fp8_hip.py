@@ -63,7 +63,7 @@ def _site_weight(block, site: str):  # noqa: ANN001,ANN202
 
 
 def block_want(block, sites=SITES) -> dict:  # noqa: ANN001
-    """{(weight data_ptr, weight shape): site} for this block's FP8 qkv / out / fc1 weights."""
+    """The block's FP8 qkv / out / fc1 weights as the router looks them up: weight key -> site."""
     found = ((site, _site_weight(block, site)) for site in sites)
     return {weight_key(w): site for site, w in found if w is not None}
 

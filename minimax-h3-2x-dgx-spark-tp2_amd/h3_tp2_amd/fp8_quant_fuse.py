@@ -186,14 +186,22 @@ class ProducerScope:
             return
         p.materialize()
         _stats["materialize"] += 1
-        _notes.once("mat-" + reason, "%s: %s stash materialised (stock producer into the placeholder)", reason, p.site)
+        _notes.once("mat-" + reason, "%s: the %s stash is replaced by the stock producer's bf16 row", reason, p.site)
 
     def open_for(self, site: str) -> bool:
         """True when ``site`` is planned and enabled; a stash still waiting is materialised first."""
         if site not in self.plan or site in _state["disabled"]:
             return False
-        self.release(f"{site} producer while another stash was pending")
+        self.release(f"the {site} producer ran while an earlier stash still waited")
         return True
+
+    def close(self) -> None:
+        """The block returned: a stash nobody consumed gets its bf16 row for whoever still holds the placeholder."""
+        self.release("the block returned with its stash unconsumed")
+
+    def drop(self) -> None:
+        """The block raised: nothing will read the placeholder."""
+        self.pending = None
 
 
 _Ctx = ProducerScope          # the name the protocol tests address
@@ -206,7 +214,8 @@ def _scope() -> ProducerScope | None:
 # ---- the QuantFP8 drop-in ---------------------------------------------------------------------------------------------
 
 def _stock_quant(quant_obj, h: torch.Tensor):  # noqa: ANN001,ANN202
-    """The layer's own per-token quant (the unwrapped ``QuantFP8.forward``), called as ``apply_weights`` calls it."""
+    """The per-token quant the layer would run without this module (the original ``QuantFP8.forward``), with the
+    arguments ``apply_weights`` passes."""
     return _state["orig_quant"](quant_obj, h, None, None)
 
 
@@ -239,7 +248,7 @@ def make_quant_forward(orig):  # noqa: ANN001,ANN201
                     _verify(waiting)
                 _stats["consumed"] += 1
                 return waiting.q, waiting.scale
-            scope.release("quant of another tensor")
+            scope.release("a quant of some other tensor came first")
         if dynamic and _state["kernel1"] and dynamic_per_token(self) and kernel1_takes(x):
             _stats["kernel1"] += 1
             return quant(x)
@@ -260,7 +269,7 @@ def _layer_post_hook(module, args, output):  # noqa: ANN001,ANN202
     waiting = scope.pending if scope is not None else None
     if waiting is None or waiting.layer is not module:
         return None
-    scope.release(f"{waiting.site} layer returned without consuming")
+    scope.release(f"the {waiting.site} layer returned without taking its stash")
     _stats["rerun"] += 1
     return module.forward(*args)
 
@@ -273,59 +282,56 @@ def _quant_of(layer):  # noqa: ANN001,ANN202
     return q if cls is not None and isinstance(q, cls) and dynamic_per_token(q) and not has_static else None
 
 
-def _site_refusal(site: str, layer, lora_types) -> str | None:  # noqa: ANN001
-    """Why ``site``'s layer cannot take a stash (None: it can)."""
-    if layer is None or (lora_types and isinstance(layer, lora_types)):
-        return f"{site}: missing or LoRA-wrapped layer"
-    if getattr(layer, "tp_size", 1) != 1:
-        return f"{site}: tp_size != 1"
-    if _quant_of(layer) is None:
-        return f"{site}: not a dynamic per-token FP8 linear"
-    return None
+def _producer_refusal(site: str, layer, lora_types) -> str | None:  # noqa: ANN001
+    """Why ``site``'s layer cannot take its input from a fused producer (None: it can): the shared layer rules, and
+    its input quant must be a dynamic per-token QuantFP8 (the stash replaces exactly that call)."""
+    why = _sites.layer_refusal(site, layer, lora_types)
+    if why is None and _quant_of(layer) is None:
+        why = f"{site}: its input is not quantised dynamically per token"
+    return why
+
+
+def _site_applies(block, site: str) -> bool:
+    """The fc2 site wraps SiluAndMul: a block whose MLP activation is something else has no fc2 producer to fuse."""
+    act_cls = _state["act_cls"]
+    if site != "fc2" or act_cls is None:
+        return True
+    return isinstance(getattr(getattr(block, "mlp", None), "act_fn", None), act_cls)
+
+
+def _watch(layer) -> None:  # noqa: ANN001
+    """Hang the safety net (``_layer_post_hook``) on a planned layer, once."""
+    if not getattr(layer, "_h3_tp2_amd_quant_hook", False):
+        layer.register_forward_hook(_layer_post_hook)
+        layer._h3_tp2_amd_quant_hook = True
 
 
 def block_plan(block, sites, lora_types=()) -> tuple[dict | None, str]:  # noqa: ANN001
-    """{site: (layer, QuantFP8 instance)} for this block, or (None, reason)."""
+    """The producer sites of this block, as {site: (layer, its QuantFP8 instance)}, or (None, why not).  Every site
+    still enabled must qualify, or the block runs stock."""
     if _sites.tracing():
-        return None, "torch.compile tracing"
-    act_cls = _state["act_cls"]
-    plan: dict = {}
-    for site in (s for s in sites if s not in _state["disabled"]):
-        layer = _sites.site_layer(block, site)
-        reason = _site_refusal(site, layer, lora_types)
-        if reason is not None:
-            return None, reason
-        act = getattr(getattr(block, "mlp", None), "act_fn", None)
-        if site == "fc2" and act_cls is not None and not isinstance(act, act_cls):
-            continue                                   # the MLP's activation is not the SiluAndMul the site wraps
-        plan[site] = (layer, _quant_of(layer))
-        if not getattr(layer, "_h3_tp2_amd_quant_hook", False):
-            layer.register_forward_hook(_layer_post_hook)
-            layer._h3_tp2_amd_quant_hook = True
-    return (plan or None), "no site left"
+        return None, "inside a torch.compile trace"
+    layers = {site: _sites.site_layer(block, site) for site in sites if site not in _state["disabled"]}
+    refusals = [why for why in (_producer_refusal(site, layer, lora_types) for site, layer in layers.items()) if why]
+    if refusals:
+        return None, refusals[0]
+    plan = {site: (layer, _quant_of(layer)) for site, layer in layers.items() if _site_applies(block, site)}
+    for layer, _ in plan.values():
+        _watch(layer)
+    return (plan or None), "every site is disabled or inapplicable"
 
 
 def make_block_forward(orig_forward, sites, lora_types=()):  # noqa: ANN001,ANN201
-    """Run a DiT block's forward inside a ProducerScope (thread-local; the enclosing scope comes back afterwards); a
-    stash still waiting when the block returns is materialised."""
+    """Run a DiT block's forward inside a ProducerScope (``_sites.block_scope``: thread-local, nested blocks restore the
+    outer scope, a stash left waiting at the end is computed the stock way)."""
     @functools.wraps(orig_forward)
     def forward(self, *args, **kwargs):  # noqa: ANN001,ANN202
-        plan, reason = block_plan(self, sites, lora_types)
+        plan, why = block_plan(self, sites, lora_types)
         if plan is None:
-            _notes.once("plan-" + reason, "block not fused (%s); stock path", reason)
+            _notes.once("plan-" + why, "%s: this block's producers run stock", why)
             return orig_forward(self, *args, **kwargs)
-        scope, outer = ProducerScope(self, plan), _scope()
-        _tls.ctx = scope
-        finished = False
-        try:
-            result = orig_forward(self, *args, **kwargs)
-            finished = True
-        finally:
-            _tls.ctx = outer
-            if finished:
-                scope.release("stash left at the end of the block")
-            scope.pending = None
-        return result
+        with _sites.block_scope(_tls, ProducerScope(self, plan)):
+            return orig_forward(self, *args, **kwargs)
 
     forward._h3_tp2_amd_quant = True
     return forward
@@ -334,7 +340,7 @@ def make_block_forward(orig_forward, sites, lora_types=()):  # noqa: ANN001,ANN2
 # ---- the producer sites -----------------------------------------------------------------------------------------------
 
 def _k_of(layer) -> int:  # noqa: ANN001
-    """The layer's input width (weight [K, N] as vLLM stores it)."""
+    """K, the width of the layer's input (vLLM keeps the weight as [K, N])."""
     w = getattr(layer, "weight", None)
     return int(w.shape[0]) if isinstance(w, torch.Tensor) and w.dim() == 2 else -1
 
@@ -550,7 +556,7 @@ def make_gate_rms_wrapper(orig):  # noqa: ANN001,ANN201
 
 
 def make_act_forward(orig):  # noqa: ANN001,ANN201
-    """``SiluAndMul.forward`` (the MLP's act_fn on fc1's bf16 output): the fc2 site."""
+    """The fc2 site's producer: the MLP's ``SiluAndMul.forward`` (act_fn, applied to fc1's bf16 output)."""
     def forward(self, x):  # noqa: ANN001,ANN202
         out = _engage(_SiluMulCall(self, x), orig)
         return out if out is not None else orig(self, x)

@@ -58,7 +58,8 @@ def scale_swiglu_quant(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bi
 
 def gemm_swiglu(a: torch.Tensor, b: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor,
                 bias: torch.Tensor | None) -> torch.Tensor:
-    """fc1 + epilogue + SwiGLU in one kernel: bf16 [M, N/2] from fp8 a [M, K], b [K, N] (b.t() contiguous)."""
+    """Kernel 3 on fc1's operands (fp8 a [M, K], b [K, 2F] with b.t() contiguous): the MLP's hidden row h, bf16
+    [M, F], with the GEMM epilogue and the SwiGLU applied in registers."""
     return ops.gemm_swiglu(a, b.t(), sa.reshape(-1), sb.reshape(-1), _bias(bias))
 
 
