@@ -478,11 +478,24 @@ __device__ __forceinline__ uint32_t max_abs_f16x2(uint32_t m, uint32_t p) {
     return m > hi ? m : hi;
 }
 
-// x + 0: -0 becomes +0 (round to nearest), every other value (NaN included) is unchanged.
-__device__ __forceinline__ float zero_to_pos(float x) {
+// Running maxima of |x| over packed bf16 pairs, one per 16-bit half: with the sign bit cleared, bf16 magnitudes order
+// as their bit patterns (NaN patterns above inf), so a pair costs one mask and one packed u16 max.  pk_max_f32 folds
+// the two halves into the fp32 bit pattern of the larger, the value max_abs_bf16x2 accumulates over the same pairs.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 max_abs_pk(u16x2 m, uint32_t p) {
+    return __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, p & 0x7fff7fffu));
+}
+__device__ __forceinline__ uint32_t pk_max_f32(u16x2 m) {
+    const uint32_t a = m[0], b = m[1];
+    return (a > b ? a : b) << 16;
+}
+
+// A +0 the compiler cannot see through, made once per epilogue: x + z turns -0 into +0 (round to nearest) and leaves
+// every other value (NaN included) unchanged, and the add is not folded away.
+__device__ __forceinline__ float opaque_zero() {
     float z = 0.0f;
-    asm volatile("" : "+v"(z));                         // an opaque zero: the add is not folded away
-    return x + z;
+    asm volatile("" : "+v"(z));
+    return z;
 }
 
 // ---- epilogue ----
@@ -567,6 +580,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                 sbu_v[t][q] = *reinterpret_cast<const v4f*>(sb_l + 128 + wn * 64 + 32 * t + 8 * q + 4 * hi);
             }
         const uint16_t* silu_l = reinterpret_cast<const uint16_t*>(lds + Lds<EPI>::SILU_OFF);
+        const float zero = opaque_zero();
         // 16 staged token rows to their output rows: 16 bytes per lane, 8 rows per store instruction
         auto flush16 = [&](int m0, int c0, int ncols) {
             const int c = lane & 7;
@@ -586,8 +600,12 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
         for (int j = 0; j < 4; ++j) {
             const int m = mrow0 + 32 * j + mj;
             const float sam = sa_j[j];
-            // gate and up of the pass rounded to bf16 (packed: gate low, up high)
-            uint32_t gu[2][4][4], sl[2][4][4];
+            // gate and up of the pass rounded to bf16.  The gate is converted into both halves of a word, so that its
+            // table key (the bf16 bits rotated left by one: the sign lands in bit 0 and both signs form one range) is
+            // the bit field [15, 31) of that word; the up value goes to the high half over a zero low half, which is
+            // its fp32 value.
+            uint32_t key[2][4][4], uu[2][4][4], sl[2][4][4];
+            uint64_t outside = 0;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -608,25 +626,15 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                         const float tu = sbu_v[t][q][r] * acc[t + 2][j][4 * q + r];
                         const float gy = HAS_BIAS ? __builtin_fmaf(sam, tg, bg[r]) : sam * tg;
                         const float uy = HAS_BIAS ? __builtin_fmaf(sam, tu, bu[r]) : sam * tu;
-                        gu[t][q][r] = cvt_bf16x2(gy, uy);
+                        const uint32_t rk = (cvt_bf16x2(gy, gy) >> 15) & 0xffffu;
+                        uu[t][q][r] = cvt_bf16x2(0.0f, uy);
+                        // the compact table's index; a key outside its range wraps to a large value
+                        key[t][q][r] = rk - H3_SILU_ROT_R0;
+                        outside |= __ballot(key[t][q][r] >= (uint32_t)H3_SILU_ROT_LEN);
                     }
                 }
             // bf16(g/(1+exp(-g))) of every gate of the pass: from the compact table in LDS when every key of the pass
-            // lies in its range (the rotated key clamped to the range equals the key), else from the full table
-            uint32_t key[2][4][4];
-            uint64_t outside = 0;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint32_t g = gu[t][q][r];
-                        const uint32_t rk = ((g << 1) & 0xfffeu) | ((g >> 15) & 1u);
-                        const uint32_t ck = min(max(rk, H3_SILU_ROT_R0), H3_SILU_ROT_R0 + H3_SILU_ROT_LEN - 1u);
-                        outside |= __ballot(ck != rk);
-                        key[t][q][r] = ck - H3_SILU_ROT_R0;
-                    }
+            // lies in its range, else from the full table (indexed by the gate's bf16 bits, the key rotated back)
             if (outside == 0) {
 #pragma unroll
                 for (int t = 0; t < 2; ++t)
@@ -640,27 +648,39 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) sl[t][q][r] = p.silu[gu[t][q][r] & 0xffffu];
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t rk = (key[t][q][r] + H3_SILU_ROT_R0) & 0xffffu;
+                            sl[t][q][r] = p.silu[(rk >> 1) | ((rk & 1u) << 15)];
+                        }
             }
-            uint32_t rmax = 0;
             uint32_t hp[2][4][2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int cl = 32 * t + 8 * q + 4 * hi;
-                    const bool ok = col0 + cl < F && m < p.M;
                     float hv[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float u = zero_to_pos(u2f(gu[t][q][r] & 0xffff0000u));   // -0 up -> +0 (fp8_swiglu.py:66)
-                        hv[r] = bf16_to_f32(sl[t][q][r]) * u;
-                    }
+                    for (int r = 0; r < 4; ++r)                    // -0 up -> +0 (fp8_swiglu.py:66)
+                        hv[r] = bf16_to_f32(sl[t][q][r]) * (u2f(uu[t][q][r]) + zero);
                     hp[t][q][0] = cvt_bf16x2(hv[0], hv[1]);
                     hp[t][q][1] = cvt_bf16x2(hv[2], hv[3]);
-                    if (ok) rmax = max_abs_bf16x2(max_abs_bf16x2(rmax, hp[t][q][0]), hp[t][q][1]);
                 }
+            // the row maximum over the columns before F (rows past M are dropped by row_amax)
+            u16x2 mx2 = {0, 0};
+            if (col0 + 64 <= F) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) mx2 = max_abs_pk(max_abs_pk(mx2, hp[t][q][0]), hp[t][q][1]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (col0 + 32 * t + 8 * q + 4 * hi < F)
+                            mx2 = max_abs_pk(max_abs_pk(mx2, hp[t][q][0]), hp[t][q][1]);
             }
+            const uint32_t rmax = pk_max_f32(mx2);
             if (p.row_amax) row_amax(rmax, m);
             // the pass's 32 token rows through the 16-row staging area, one half at a time (this wave's LDS accesses
             // complete in order, so the second half's writes follow the first half's reads)
@@ -692,9 +712,11 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
         for (int j = 0; j < 4; ++j) {
             const int m = mrow0 + 32 * j + mj;
             const float sam = sa_j[j];
-            uint32_t rmax = 0;
+            uint32_t rmax = 0;                          // fp16 outputs: the fp32 bits of the largest |y|
+            u16x2 mx2 = {0, 0};                         // bf16 outputs: |y| bit patterns, one per half
 #pragma unroll
             for (int ip = 0; ip < NI / 2; ++ip) {
+                const bool all_cols = col0 + 64 * ip + 64 <= p.N;     // wave-uniform: no column of the pass is past N
                 wave_sync();                            // the previous flush's reads before these writes
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii) {
@@ -725,16 +747,17 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                             lo = cvt_bf16x2(v[0], v[1]);
                             hi2 = cvt_bf16x2(v[2], v[3]);
                         }
-                        if (EPI == EPI_AMAX && ok)
-                            rmax = OUT_DT ? max_abs_f16x2(max_abs_f16x2(rmax, lo), hi2)
-                                          : max_abs_bf16x2(max_abs_bf16x2(rmax, lo), hi2);
+                        // the row maximum over the columns before N (rows past M are dropped by row_amax)
+                        if (EPI == EPI_AMAX && OUT_DT && ok) rmax = max_abs_f16x2(max_abs_f16x2(rmax, lo), hi2);
+                        if (EPI == EPI_AMAX && !OUT_DT && (all_cols || n < p.N))
+                            mx2 = max_abs_pk(max_abs_pk(mx2, lo), hi2);
                         put4(mj, cl, lo, hi2);
                     }
                 }
                 wave_sync();                            // every lane's writes before any lane's reads
                 flush(mrow0 + 32 * j, col0 + 64 * ip, p.N);
             }
-            if (EPI == EPI_AMAX) row_amax(rmax, m);
+            if (EPI == EPI_AMAX) row_amax(OUT_DT ? rmax : pk_max_f32(mx2), m);
         }
     }
 }
