@@ -14,7 +14,8 @@
 //     across the wave with xor-shuffles -- no LDS, no barrier;
 //   * scale and 1/scale are IEEE fp32 divisions (hipcc's correctly rounded divide), computed once per lane;
 //   * the e4m3 conversion is gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn, RNE), 8-byte stores per chunk.
-// Four rows per 256-thread workgroup; rows beyond M exit before any memory access.
+// Four rows per 256-thread workgroup (two when a row is split over two waves, below); rows beyond M exit before
+// any memory access.
 #include "h3fp8_common.h"
 
 namespace {
@@ -57,15 +58,19 @@ __device__ __forceinline__ uint2 chunk_quant(uint4 v, float inv) {
     return make_uint2(e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7]));
 }
 
-// One wave per row, CPL 16-byte chunks per lane held in registers.  KNOWN_AMAX: the row maximum comes from row_amax
-// (fp32 bits) instead of the row.
-template <int CPL, bool KNOWN_AMAX>
+// WPR waves per row, CPL 16-byte chunks per lane held in registers: wave p of a row owns its chunks
+// 64 CPL p .. 64 CPL (p + 1) - 1.  KNOWN_AMAX: the row maximum comes from row_amax (fp32 bits) instead of the row, so
+// the waves of a row are independent; the row's own maximum needs the whole row in one wave (WPR = 1).
+template <int CPL, bool KNOWN_AMAX, int WPR = 1>
 __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
                                                          int64_t K, uint8_t* __restrict__ q, int64_t ldq,
                                                          float* __restrict__ scale,
                                                          const float* __restrict__ row_amax) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    static_assert(WPR == 1 || (KNOWN_AMAX && 4 % WPR == 0), "a row split over waves needs its maximum given");
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row = (int64_t)blockIdx.x * (4 / WPR) + wave / WPR;
+    // the lane's first chunk is lane + 64 CPL p; chunk j of the lane is that + 64 j
+    const int lane = (threadIdx.x & 63) + 64 * CPL * (wave % WPR);
     if (row >= M) return;
     // Range-checked buffer accesses: chunks past the row read as zero (|0| does not raise the maximum) and their
     // stores are dropped, with no branch -- every load of the row is in flight at once.
@@ -146,8 +151,18 @@ int launch_quant(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int6
     dim3 grid((unsigned)((M + 3) / 4)), block(256);
     const uint16_t* xp = (const uint16_t*)x;
     uint8_t* qp = (uint8_t*)q;
-#define H3_Q(N)                                                                                              \
-    hipLaunchKernelGGL((quant_rows_kernel<N, KNOWN>), grid, block, 0, st, xp, ldx, M, K, qp, ldq, scale, row_amax)
+    // With the maximum given, rows of 6 or more chunks per lane go to two waves of half the chunks each: half the
+    // registers per wave, twice the waves in flight (measured at M = 91 728: K = 8192 427 -> 383 us, K = 3072
+    // 129.7 -> 127.7 us; four waves of a quarter measure the same as two)
+#define H3_Q(N)                                                                                                        \
+    do {                                                                                                               \
+        if constexpr (KNOWN && N >= 6)                                                                                 \
+            hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2>), dim3((unsigned)((M + 1) / 2)), block, 0, st, xp,  \
+                               ldx, M, K, qp, ldq, scale, row_amax);                                                   \
+        else                                                                                                           \
+            hipLaunchKernelGGL((quant_rows_kernel<N, KNOWN>), grid, block, 0, st, xp, ldx, M, K, qp, ldq, scale,       \
+                               row_amax);                                                                              \
+    } while (0)
     if (cpl <= 1) H3_Q(1);
     else if (cpl <= 2) H3_Q(2);
     else if (cpl <= 3) H3_Q(3);

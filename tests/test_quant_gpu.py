@@ -102,14 +102,24 @@ def test_quant_strided_rows_and_empty(cuda):
     assert q0.shape == (0, 3072) and s0.shape == (0, 1)
 
 
-def test_quant_rows_amax_tail(cuda):
-    """The tail pass with the row maxima given equals the full quant."""
+@pytest.mark.parametrize("M,K", [(257, 8192), (3, 3072), (129, 3000), (64, 4096), (33, 6144), (5, 8200),
+                                 (7, 16384), (2, 1536), (9, 512)])
+def test_quant_rows_amax_tail(cuda, M, K):
+    """The tail pass with the row maxima given equals the full quant: one wave per row (K <= 2560) and a row split over
+    two waves (3 .. 16 chunks per lane each), odd row counts (half of the last workgroup idle) and ragged widths."""
     from h3_tp2_amd import ops
-    x = torch.randn(257, 8192, generator=torch.Generator().manual_seed(4)).to(BF16)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(4 + K)).to(BF16)
+    x[0, K - 1] = 300.0                                 # the maximum in the row's last chunk (the second wave's part)
     amax = x.float().abs().amax(dim=1)
-    q, s = ops.quant_rows_amax(x.to(cuda), amax.to(cuda))
+    guard = 4096
+    buf = torch.full((M * K + 2 * guard,), 0x5a, dtype=torch.uint8, device=cuda)
+    q = buf[guard:guard + M * K].view(M, K)
+    s = torch.full((M + 1,), -1.0, device=cuda)
+    rc = ops.quant_rows_amax(x.to(cuda), amax.to(cuda), q=q.view(torch.float8_e4m3fn), scale=s[:M].view(M, 1))
     torch.cuda.synchronize()
-    assert_quant_equal(q, s, *oracle_quant(x))
+    assert_quant_equal(rc[0], rc[1], *oracle_quant(x))
+    assert bool((buf[:guard] == 0x5a).all()) and bool((buf[-guard:] == 0x5a).all())
+    assert float(s[M]) == -1.0
 
 
 def test_quant_rejects_bad_arguments(cuda):
