@@ -5,17 +5,17 @@
 //   q_k = e4m3fn_rne(clamp(x_k * (1 / scale), -448, 448)).
 //
 // Design (HBM-bound: 2 bytes read + 1 byte written per element, plus 4 bytes of scale per row):
-//   * one 64-lane wavefront per row; a lane owns CPL chunks of 8 bf16 (16-byte loads), chunk c = lane + 64 j, so every
-//     load instruction of the wave reads 1 KiB of the row contiguously; the row stays in VGPRs (read from HBM once);
+//   * one 64-lane wavefront per row, or two for rows of 6+ chunks per lane; a lane owns CPL chunks of 8 bf16 (16-byte
+//     loads), chunk c = lane + 64 j, so every load instruction of a wave reads 1 KiB of the row contiguously; the row
+//     stays in VGPRs (read from HBM once);
 //   * range-checked buffer loads and stores (a per-row descriptor): no branch around the row's tail, so all of a
 //     row's loads are in flight together (guarded global loads made the compiler wait after every second load);
 //   * the row maximum is an integer max over |x| bit patterns (for non-negative floats the integer order is the float
 //     order and every NaN pattern is above +inf, so the max propagates NaN exactly like the reference's), reduced
-//     across the wave with xor-shuffles -- no LDS, no barrier;
+//     across the wave with xor-shuffles (and between the two waves of a split row through LDS);
 //   * scale and 1/scale are IEEE fp32 divisions (hipcc's correctly rounded divide), computed once per lane;
 //   * the e4m3 conversion is gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn, RNE), 8-byte stores per chunk.
-// Four rows per 256-thread workgroup (two when a row is split over two waves, below); rows beyond M exit before
-// any memory access.
+// Four rows per 256-thread workgroup (two when a row is split over two waves, below); rows beyond M touch no memory.
 #include "h3fp8_common.h"
 
 namespace {
@@ -60,21 +60,24 @@ __device__ __forceinline__ uint2 chunk_quant(uint4 v, float inv) {
 
 // WPR waves per row, CPL 16-byte chunks per lane held in registers: wave p of a row owns its chunks
 // 64 CPL p .. 64 CPL (p + 1) - 1.  KNOWN_AMAX: the row maximum comes from row_amax (fp32 bits) instead of the row, so
-// the waves of a row are independent; the row's own maximum needs the whole row in one wave (WPR = 1).
+// the waves of a row are independent; otherwise two waves of a row exchange their maxima through LDS (one barrier),
+// and no wave leaves before it: a wave of a row at or past M reads and writes nothing (empty buffer ranges).
 template <int CPL, bool KNOWN_AMAX, int WPR = 1>
 __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
                                                          int64_t K, uint8_t* __restrict__ q, int64_t ldq,
                                                          float* __restrict__ scale,
                                                          const float* __restrict__ row_amax) {
-    static_assert(WPR == 1 || (KNOWN_AMAX && 4 % WPR == 0), "a row split over waves needs its maximum given");
+    static_assert(WPR == 1 || WPR == 2, "one or two waves per row");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t row = (int64_t)blockIdx.x * (4 / WPR) + wave / WPR;
     // the lane's first chunk is lane + 64 CPL p; chunk j of the lane is that + 64 j
     const int lane = (threadIdx.x & 63) + 64 * CPL * (wave % WPR);
-    if (row >= M) return;
+    constexpr bool SHARED_MAX = WPR == 2 && !KNOWN_AMAX;
+    if (!SHARED_MAX && row >= M) return;
+    const bool live = row < M;
     // Range-checked buffer accesses: chunks past the row read as zero (|0| does not raise the maximum) and their
     // stores are dropped, with no branch -- every load of the row is in flight at once.
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + row * ldx, (uint32_t)K * 2u);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + (live ? row : 0) * ldx, live ? (uint32_t)K * 2u : 0u);
     uint4 v[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -92,11 +95,18 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restr
             m = m > c ? m : c;
         }
         m = wave_max_u32(m);
+        if (SHARED_MAX) {
+            __shared__ uint32_t part[4];
+            part[wave] = m;
+            __syncthreads();
+            const uint32_t o = part[wave ^ 1];
+            m = m > o ? m : o;
+        }
         amax = u2f(m << 16);
     }
     const float s = row_scale(amax);
     const float inv = inv_scale(s);
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + row * ldq, (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + (live ? row : 0) * ldq, live ? (uint32_t)K : 0u);
     if (__builtin_amdgcn_readfirstlane(f2u(amax) & 0x7fffffffu) < 0x7f800000u) {   // wave-uniform: finite maximum
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
@@ -110,7 +120,7 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restr
             __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
         }
     }
-    if (lane == 0) scale[row] = s;
+    if (live && lane == 0) scale[row] = s;
 }
 
 // Rows too wide for the register-resident form: the row is read twice (max pass, then quant pass).
@@ -151,12 +161,12 @@ int launch_quant(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int6
     dim3 grid((unsigned)((M + 3) / 4)), block(256);
     const uint16_t* xp = (const uint16_t*)x;
     uint8_t* qp = (uint8_t*)q;
-    // With the maximum given, rows of 6 or more chunks per lane go to two waves of half the chunks each: half the
-    // registers per wave, twice the waves in flight (measured at M = 91 728: K = 8192 427 -> 383 us, K = 3072
-    // 129.7 -> 127.7 us; four waves of a quarter measure the same as two)
+    // Rows of 6 or more chunks per lane go to two waves of half the chunks each: half the registers per wave, twice
+    // the waves in flight (measured at M = 91 728: with the maximum given K = 8192 427 -> 383 us, K = 3072
+    // 129.7 -> 127.7 us, four waves of a quarter the same as two; the full quant at K = 3072 128.5 -> 125.0 us)
 #define H3_Q(N)                                                                                                        \
     do {                                                                                                               \
-        if constexpr (KNOWN && N >= 6)                                                                                 \
+        if constexpr (N >= 6)                                                                                          \
             hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2>), dim3((unsigned)((M + 1) / 2)), block, 0, st, xp,  \
                                ldx, M, K, qp, ldq, scale, row_amax);                                                   \
         else                                                                                                           \
