@@ -17,7 +17,9 @@
 // range-checked buffer load (no branches, so all of a row's loads are in flight together): the row's own loads go
 // out first, then the index and, up to 8 chunks per lane, every weight / shift / scale chunk before the reduction.
 // HBM traffic is 3H + 4 bytes per row (7H + 4 for the gate form); the weight and table rows (3 x 2H bytes per row)
-// come from L2.  Staging the tables in LDS per persistent workgroup was measured slower (fewer rows in flight).
+// come from L2.  Staging the tables in LDS per persistent workgroup was measured slower (fewer rows in flight); the
+// qkv-site form with 4-8 chunks per lane instead stages them once per 8-row workgroup as fp32 values
+// (rms_mod_quant_staged_kernel below).
 //
 // An index outside [0, n_index) reads table row 0 instead (no access out of bounds) and poisons the row: residual_out
 // and h are NaN, the scale NaN, the codes NaN -- torch's index_select would raise; a kernel cannot.
@@ -318,6 +320,152 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     });
 }
 
+// The qkv-site producer (no gate, bf16 x) with its tables staged in LDS as fp32: eight rows per 512-thread workgroup,
+// one wave per row.  The modulation tables have one row per sample, so nearly every workgroup's rows share one index:
+// the workgroup converts the weight row and the scale / shift rows of its first row's index once into fp32 LDS tables
+// of w, 1 + scale and shift (the same fp32 values the per-element arithmetic forms: bf16 -> fp32 is exact, 1 + scale
+// the same fp32 add), and a wave whose row has that index reads them there at the point of use -- three unpacks and
+// an add fewer per element, and no table chunk held in registers.  A wave whose row has another index (a sample
+// boundary inside the workgroup, or an index outside the tables) reads its tables from global memory one chunk at a
+// time.  Arithmetic and order otherwise as rms_mod_quant_row, so the outputs are bitwise the same.  Measured at
+// H = 3072, M = 16 740 with the indices in runs (one per sample): 37.3 -> 33.6 us; with a random index per row
+// (almost every wave on the global path) 37.5 -> 44.1 us.
+// LDS: table t (0 w, 1 1 + scale, 2 shift), half s (elements 0-3 / 4-7 of a chunk), chunk c: tabs[t][s][c] (float4),
+// so a wave's 16-byte reads of one half are contiguous (no bank conflicts).
+template <int OUT, int CPL, bool FULL>
+__global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
+    constexpr bool QUANT = (OUT & 1) != 0, WRITE_H = (OUT & 2) != 0;
+    constexpr int NC = 64 * CPL;                        // 16-byte chunks per table row (past H: zeros)
+    static_assert(NC <= 512, "one staging load per thread and table");
+    __shared__ v4f tabs[3][2][NC];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t m0 = (int64_t)blockIdx.x * 8, m = m0 + wave;
+    const bool live = m < a.M;
+    // the indices first (scalar loads), then the row's own loads, then the staging loads
+    bool bad, bad0;
+    const int64_t i = row_index(a, live ? m : m0, bad);
+    const int64_t i0 = row_index(a, m0, bad0);
+    const uint32_t rb = (uint32_t)a.H * 2u;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (live ? m : m0) * a.ldx, live ? rb : 0u);
+    v4u xv[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) xv[j] = ld16<2>(xr, lane + 64 * j);     // streamed once: non-temporal
+    if (tid < NC) {                                     // wave-uniform (NC is a multiple of 64)
+        const v4u w = ld16(make_rsrc(a.weight, rb), tid);
+        const v4u sc = ld16(make_rsrc(a.scale + i0 * a.ld_scale, rb), tid);
+        const v4u sh = ld16(make_rsrc(a.shift + i0 * a.ld_shift, rb), tid);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            v4f wf, gf, bf;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = 2 * s + (e >> 1);
+                const bool hi = e & 1;
+                wf[e] = u2f(hi ? (w[k] & 0xffff0000u) : (w[k] << 16));
+                gf[e] = 1.0f + u2f(hi ? (sc[k] & 0xffff0000u) : (sc[k] << 16));
+                bf[e] = u2f(hi ? (sh[k] & 0xffff0000u) : (sh[k] << 16));
+            }
+            tabs[0][s][tid] = wf;
+            tabs[1][s][tid] = gf;
+            tabs[2][s][tid] = bf;
+        }
+    }
+    __syncthreads();
+    if (!live) return;
+    const bool staged = !bad && i == i0;                // wave-uniform
+    // sum of squares: each square exact in fp32, the fp64 sum in lane order, rounded once to fp32
+    double ss = 0.0;
+    float xf[CPL][8];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float f0 = u2f(xv[j][k] << 16), f1 = u2f(xv[j][k] & 0xffff0000u);
+            xf[j][2 * k] = f0;
+            xf[j][2 * k + 1] = f1;
+            ss += (double)(f0 * f0);
+            ss += (double)(f1 * f1);
+        }
+    ss = wave_sum_f64(ss);
+    const float hf = (float)a.H;
+    float var = (float)ss;
+    asm volatile("" : "+v"(var));                       // the division by H stays a division
+    var = var / hf;
+    const float d = __builtin_sqrtf(var + a.eps);
+    float one = 1.0f;
+    asm volatile("" : "+v"(one));
+    const float r = bad ? u2f(0x7fc00000u) : one / d;
+    const int nchunk = (int)(a.H >> 3);
+    v4u h[CPL];
+    u16x2 mx2 = {0, 0};
+    if (staged) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = lane + 64 * j;
+            const bool in = FULL || c < nchunk;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const v4f wf = tabs[0][s][c], gf = tabs[1][s][c], bf = tabs[2][s][c];
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float n = (xf[j][4 * s + e] * r) * wf[e];
+                    o[e] = n * gf[e] + bf[e];
+                }
+                h[j][2 * s] = in ? cvt_bf16x2(o[0], o[1]) : 0u;
+                h[j][2 * s + 1] = in ? cvt_bf16x2(o[2], o[3]) : 0u;
+            }
+            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][0] & 0x7fff7fffu));
+            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][1] & 0x7fff7fffu));
+            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][2] & 0x7fff7fffu));
+            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][3] & 0x7fff7fffu));
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t tw = make_rsrc(a.weight, rb);
+        const __amdgpu_buffer_rsrc_t tsc = make_rsrc(a.scale + i * a.ld_scale, rb);
+        const __amdgpu_buffer_rsrc_t tsh = make_rsrc(a.shift + i * a.ld_shift, rb);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = lane + 64 * j;
+            const bool in = FULL || c < nchunk;
+            const v4u wv = ld16(tw, c), sc = ld16(tsc, c), sh = ld16(tsh, c);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float o[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float we = u2f(e ? (wv[k] & 0xffff0000u) : (wv[k] << 16));
+                    const float se = u2f(e ? (sc[k] & 0xffff0000u) : (sc[k] << 16));
+                    const float be = u2f(e ? (sh[k] & 0xffff0000u) : (sh[k] << 16));
+                    const float n = (xf[j][2 * k + e] * r) * we;
+                    const float g = one + se;
+                    o[e] = n * g + be;
+                }
+                h[j][k] = in ? cvt_bf16x2(o[0], o[1]) : 0u;
+                mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][k] & 0x7fff7fffu));
+            }
+            __builtin_amdgcn_sched_barrier(0);          // one chunk's table loads in flight at a time
+        }
+    }
+    uint32_t mx = (uint32_t)(mx2[0] > mx2[1] ? mx2[0] : mx2[1]) << 16;
+    float s = 0.0f;
+    if (QUANT) {
+        mx = wave_max_u32(mx);
+        s = row_scale(u2f(mx));
+        const float inv = inv_scale(s);
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + m * a.ldq, (uint32_t)a.H);
+        if (__builtin_amdgcn_readfirstlane(mx) < 0x7f800000u) store_q<CPL, true>(h, inv, qr, lane);
+        else store_q<CPL, false>(h, inv, qr, lane);
+    }
+    if (WRITE_H) {
+        const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.h_out + m * a.ldh, rb);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) st16(h[j], hr, lane + 64 * j);
+    }
+    if (QUANT && lane == 0) a.qscale[m] = s;
+}
+
 template <bool GATE, int OUT, int CPL, bool B32>
 int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
@@ -329,9 +477,23 @@ int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
     return H3FP8_OK;
 }
 
+template <int OUT, int CPL>
+int launch_rms_staged(const RmsArgs& a, hipStream_t st) {
+    const dim3 grid((unsigned)((a.M + 7) / 8)), block(512);
+    if (a.H == 512 * CPL)
+        hipLaunchKernelGGL((rms_mod_quant_staged_kernel<OUT, CPL, true>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((rms_mod_quant_staged_kernel<OUT, CPL, false>), grid, block, 0, st, a);
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
 template <bool GATE, int OUT, bool B32 = false>
 int launch_rms(const RmsArgs& a, hipStream_t st) {
     const int64_t cpl = ((a.H >> 3) + 63) / 64;
+    if (!GATE && !B32 && cpl > 2 && cpl <= 4) return launch_rms_staged<OUT, 4>(a, st);
+    if (!GATE && !B32 && cpl > 4 && cpl <= 6) return launch_rms_staged<OUT, 6>(a, st);
+    if (!GATE && !B32 && cpl > 6 && cpl <= 8) return launch_rms_staged<OUT, 8>(a, st);
     if (cpl <= 2) return launch_rms_cpl<GATE, OUT, 2, B32>(a, st);
     if (cpl <= 4) return launch_rms_cpl<GATE, OUT, 4, B32>(a, st);
     if (cpl <= 6) return launch_rms_cpl<GATE, OUT, 6, B32>(a, st);

@@ -132,6 +132,38 @@ def test_index_out_of_range_poisons_only_its_row(cuda):
         assert torch.isnan(sf[m]).item() and ((qb[m] & 0x7F) == 0x7F).all()
 
 
+@pytest.mark.parametrize("M,H", [(1003, 3072), (61, 4096), (130, 2048), (45, 2560), (77, 1536), (29, 3000)])
+def test_rms_quant_index_runs(cuda, M, H):
+    """The qkv-site producer over index runs (one index per sample, as the model calls it): the 8-row workgroups whose
+    rows share their first row's index read the tables staged in LDS, the workgroups that straddle a run boundary
+    read the other rows' tables from global memory.  Runs of 1, 3, 5, 8, 13 and long ones, an index outside the tables
+    at a workgroup's first row and inside one; every other row bit-exact against the oracle, h included."""
+    from h3_tp2_amd import ops
+    x, w, sh, sc, _, _ = mod_inputs(M, H, seed=M * 7 + H, B=5)
+    x = _directed(x)
+    runs = [1, 3, 5, 8, 13, 2, 40, 7, 9, 100]
+    vals, k = [], 0
+    while len(vals) < M:
+        vals += [k % 5] * runs[k % len(runs)]
+        k += 1
+    idx = torch.tensor(vals[:M], dtype=torch.int64)
+    bad = idx.clone()
+    poisoned = [m for m in (16, 21) if m < M]
+    for m in poisoned:
+        bad[m] = 5 if m == 16 else -3
+    ph = torch.full((M, H), float("nan"), dtype=BF16, device=cuda)
+    q, s = ops.rms_quant(x.to(cuda), w.to(cuda), *_tables(cuda, sh, sc), bad.to(cuda), EPS, ph)
+    torch.cuda.synchronize()
+    ok = [m for m in range(M) if m not in poisoned]
+    h_ref, q_ref, s_ref = O.rms_quant(bits16(x[ok]), bits16(w), bits16(sh), bits16(sc), idx[ok].numpy(), EPS)
+    qb, sf = q.view(torch.uint8).cpu(), s.cpu()
+    assert_quant_equal(qb[ok], sf[ok], q_ref, s_ref)
+    _nan_aware_equal(bits16(ph)[ok], h_ref, "h")
+    for m in poisoned:
+        assert ((bits16(ph)[m] & 0x7FFF) > 0x7F80).all()
+        assert torch.isnan(sf[m]).item() and ((qb[m] & 0x7F) == 0x7F).all()
+
+
 def test_argument_errors(cuda):
     from h3_tp2_amd import _lib, ops
     x, w, sh, sc, _, idx = mod_inputs(4, 1004, seed=13)                   # H % 8 != 0
