@@ -320,60 +320,154 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     });
 }
 
-// The qkv-site producer (no gate, bf16 x) with its tables staged in LDS as fp32: eight rows per 512-thread workgroup,
+// The producers and the out consumer with their tables staged in LDS as fp32: eight rows per 512-thread workgroup,
 // one wave per row.  The modulation tables have one row per sample, so nearly every workgroup's rows share one index:
-// the workgroup converts the weight row and the scale / shift rows of its first row's index once into fp32 LDS tables
-// of w, 1 + scale and shift (the same fp32 values the per-element arithmetic forms: bf16 -> fp32 is exact, 1 + scale
-// the same fp32 add), and a wave whose row has that index reads them there at the point of use -- three unpacks and
-// an add fewer per element, and no table chunk held in registers.  A wave whose row has another index (a sample
-// boundary inside the workgroup, or an index outside the tables) reads its tables from global memory one chunk at a
-// time.  Arithmetic and order otherwise as rms_mod_quant_row, so the outputs are bitwise the same.  Measured at
-// H = 3072, M = 16 740 with the indices in runs (one per sample): 37.3 -> 33.6 us; with a random index per row
-// (almost every wave on the global path) 37.5 -> 44.1 us.
-// LDS: table t (0 w, 1 1 + scale, 2 shift), half s (elements 0-3 / 4-7 of a chunk), chunk c: tabs[t][s][c] (float4),
-// so a wave's 16-byte reads of one half are contiguous (no bank conflicts).
-template <int OUT, int CPL, bool FULL>
+// the workgroup converts once into fp32 LDS tables the weight row, 1 + scale and shift of its first row's index, and
+// for the gated forms gate of that index, for the fp32-branch form sb and the bias (the same fp32 values the
+// per-element arithmetic forms: bf16 -> fp32 is exact, 1 + scale the same fp32 add).  A wave whose row has that index
+// reads every table there at the point of use -- unpacks and an add fewer per element, and no table chunk held in
+// registers.  A wave whose row has another index (a sample boundary inside the workgroup, or an index outside the
+// tables) reads the index-dependent tables (gate, scale, shift) from global memory one chunk at a time.  Arithmetic
+// and order otherwise as rms_mod_quant_row, so the outputs are bitwise the same.
+// LDS: table t, half s (elements 0-3 / 4-7 of a chunk), chunk c: tabs[t][s][c] (float4), so a wave's 16-byte reads
+// of one half are contiguous (no bank conflicts).  Tables: T_W weight, T_G 1 + scale, T_B shift, T_GATE gate,
+// T_SB sb, T_BIAS bias (zeros without one).
+template <bool GATE, bool B32, int OUT, int CPL, bool FULL>
 __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
     constexpr bool QUANT = (OUT & 1) != 0, WRITE_H = (OUT & 2) != 0;
-    constexpr int NC = 64 * CPL;                        // 16-byte chunks per table row (past H: zeros)
+    constexpr int NC = 64 * CPL;                        // 16-byte bf16 chunks per table row (past H: zeros)
     static_assert(NC <= 512, "one staging load per thread and table");
-    __shared__ v4f tabs[3][2][NC];
+    static_assert(GATE || !B32, "the fp32 branch belongs to the gated form");
+    constexpr int T_W = 0, T_G = 1, T_B = 2, T_GATE = 3, T_SB = GATE ? 4 : 3, T_BIAS = T_SB + 1;
+    constexpr int NT = 3 + (GATE ? 1 : 0) + (B32 ? 2 : 0);
+    __shared__ v4f tabs[NT][2][NC];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t m0 = (int64_t)blockIdx.x * 8, m = m0 + wave;
     const bool live = m < a.M;
+    const int64_t mr = live ? m : m0;                   // a row past M reads and writes nothing (empty ranges)
     // the indices first (scalar loads), then the row's own loads, then the staging loads
     bool bad, bad0;
-    const int64_t i = row_index(a, live ? m : m0, bad);
+    const int64_t i = row_index(a, mr, bad);
     const int64_t i0 = row_index(a, m0, bad0);
     const uint32_t rb = (uint32_t)a.H * 2u;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (live ? m : m0) * a.ldx, live ? rb : 0u);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + mr * a.ldx, live ? rb : 0u);
     v4u xv[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) xv[j] = ld16<2>(xr, lane + 64 * j);     // streamed once: non-temporal
+    v4u bv[GATE ? CPL : 1];
+    constexpr int NB = B32 ? CPL : 1;
+    v4u a_lo[NB], a_hi[NB];
+    if (GATE && !B32) {
+        const __amdgpu_buffer_rsrc_t br = make_rsrc(a.branch + mr * a.ld_branch, live ? rb : 0u);
+#pragma unroll
+        for (int j = 0; j < (GATE ? CPL : 1); ++j) bv[j] = ld16<2>(br, lane + 64 * j);
+    }
+    if (B32) {
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.acc + mr * a.ld_acc, live ? 2u * rb : 0u);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t c = (uint32_t)(lane + 64 * j);
+            a_lo[j] = __builtin_amdgcn_raw_buffer_load_b128(ar, c * 32u, 0, 2);
+            a_hi[j] = __builtin_amdgcn_raw_buffer_load_b128(ar, c * 32u + 16u, 0, 2);
+        }
+    }
     if (tid < NC) {                                     // wave-uniform (NC is a multiple of 64)
+        auto put = [&](int t, v4u v, bool one_plus) {   // a bf16 chunk as two fp32 halves
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                v4f f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t w = v[2 * s + (e >> 1)];
+                    const float x = u2f((e & 1) ? (w & 0xffff0000u) : (w << 16));
+                    f[e] = one_plus ? 1.0f + x : x;
+                }
+                tabs[t][s][tid] = f;
+            }
+        };
         const v4u w = ld16(make_rsrc(a.weight, rb), tid);
         const v4u sc = ld16(make_rsrc(a.scale + i0 * a.ld_scale, rb), tid);
         const v4u sh = ld16(make_rsrc(a.shift + i0 * a.ld_shift, rb), tid);
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            v4f wf, gf, bf;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int k = 2 * s + (e >> 1);
-                const bool hi = e & 1;
-                wf[e] = u2f(hi ? (w[k] & 0xffff0000u) : (w[k] << 16));
-                gf[e] = 1.0f + u2f(hi ? (sc[k] & 0xffff0000u) : (sc[k] << 16));
-                bf[e] = u2f(hi ? (sh[k] & 0xffff0000u) : (sh[k] << 16));
-            }
-            tabs[0][s][tid] = wf;
-            tabs[1][s][tid] = gf;
-            tabs[2][s][tid] = bf;
+        v4u gt = {0, 0, 0, 0}, sbl = {0, 0, 0, 0}, sbh = {0, 0, 0, 0}, bs = {0, 0, 0, 0};
+        if (GATE) gt = ld16(make_rsrc(a.gate + i0 * a.ld_gate, rb), tid);
+        if (B32) {
+            const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sb, 2u * rb);
+            sbl = __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)tid * 32u, 0, 0);
+            sbh = __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)tid * 32u + 16u, 0, 0);
+            bs = ld16(make_rsrc(a.bias ? (const void*)a.bias : (const void*)a.weight, a.bias ? rb : 0u), tid);
+        }
+        put(T_W, w, false);
+        put(T_G, sc, true);
+        put(T_B, sh, false);
+        if (GATE) put(T_GATE, gt, false);
+        if (B32) {
+            tabs[T_SB][0][tid] = __builtin_bit_cast(v4f, sbl);
+            tabs[T_SB][1][tid] = __builtin_bit_cast(v4f, sbh);
+            put(T_BIAS, bs, false);
         }
     }
     __syncthreads();
     if (!live) return;
     const bool staged = !bad && i == i0;                // wave-uniform
+    const int nchunk = (int)(a.H >> 3);
+    // the index-dependent tables of a wave off the staged index
+    const __amdgpu_buffer_rsrc_t gsc = make_rsrc(a.scale + i * a.ld_scale, rb);
+    const __amdgpu_buffer_rsrc_t gsh = make_rsrc(a.shift + i * a.ld_shift, rb);
+    const __amdgpu_buffer_rsrc_t ggt = make_rsrc(GATE ? a.gate + i * a.ld_gate : a.weight, rb);
+    if (GATE) {
+        // branch: the bf16 input, or bf16(epilogue(acc)) (t = sb * acc, then sa * t or fma(sa, t, bias), one
+        // rounding); u = bf16(residual + gate[i] * branch); residual_out = u; the norm below runs on u.  Chunks past
+        // the row are forced to +0 (their stores are dropped); an index outside the tables makes u NaN.
+        const uint32_t poison = bad ? 0x7fc07fc0u : 0u;
+        const float sam = B32 ? a.sa[m] : 0.0f;
+        const bool hb = a.bias != nullptr;
+        const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.residual_out + m * a.ld_res, rb);
+#pragma unroll
+        for (int j = 0; j < (GATE ? CPL : 1); ++j) {
+            const int c = lane + 64 * j;
+            const bool in = FULL || c < nchunk;
+            if (B32) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const v4f sbn = tabs[T_SB][s][c], bn = tabs[T_BIAS][s][c];
+                    float y[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float acc = u2f(s ? a_hi[B32 ? j : 0][e] : a_lo[B32 ? j : 0][e]);
+                        const float t = sbn[e] * acc;
+                        y[e] = hb ? __builtin_fmaf(sam, t, bn[e]) : sam * t;
+                    }
+                    bv[j][2 * s] = cvt_bf16x2(y[0], y[1]);
+                    bv[j][2 * s + 1] = cvt_bf16x2(y[2], y[3]);
+                }
+            }
+            v4u gchunk = {0, 0, 0, 0};
+            if (!staged) {
+                asm volatile("" ::: "memory");        // this chunk's gate load is not hoisted above here
+                gchunk = ld16(ggt, c);
+            }
+            v4u u;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float g0, g1;
+                if (staged) {
+                    const v4f gf = tabs[T_GATE][k >> 1][c];
+                    g0 = gf[2 * (k & 1)];
+                    g1 = gf[2 * (k & 1) + 1];
+                } else {
+                    g0 = u2f(gchunk[k] << 16);
+                    g1 = u2f(gchunk[k] & 0xffff0000u);
+                }
+                const float r0 = u2f(xv[j][k] << 16), r1 = u2f(xv[j][k] & 0xffff0000u);
+                const float p0 = g0 * u2f(bv[j][k] << 16);
+                const float p1 = g1 * u2f(bv[j][k] & 0xffff0000u);
+                u[k] = in ? (cvt_bf16x2(r0 + p0, r1 + p1) | poison) : 0u;
+            }
+            xv[j] = u;
+            st16(u, ro, c);
+        }
+    }
     // sum of squares: each square exact in fp32, the fp64 sum in lane order, rounded once to fp32
     double ss = 0.0;
     float xf[CPL][8];
@@ -396,7 +490,6 @@ __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
     float one = 1.0f;
     asm volatile("" : "+v"(one));
     const float r = bad ? u2f(0x7fc00000u) : one / d;
-    const int nchunk = (int)(a.H >> 3);
     v4u h[CPL];
     u16x2 mx2 = {0, 0};
     if (staged) {
@@ -406,7 +499,7 @@ __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
             const bool in = FULL || c < nchunk;
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const v4f wf = tabs[0][s][c], gf = tabs[1][s][c], bf = tabs[2][s][c];
+                const v4f wf = tabs[T_W][s][c], gf = tabs[T_G][s][c], bf = tabs[T_B][s][c];
                 float o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -416,26 +509,24 @@ __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
                 h[j][2 * s] = in ? cvt_bf16x2(o[0], o[1]) : 0u;
                 h[j][2 * s + 1] = in ? cvt_bf16x2(o[2], o[3]) : 0u;
             }
-            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][0] & 0x7fff7fffu));
-            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][1] & 0x7fff7fffu));
-            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][2] & 0x7fff7fffu));
-            mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][3] & 0x7fff7fffu));
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][k] & 0x7fff7fffu));
         }
     } else {
-        const __amdgpu_buffer_rsrc_t tw = make_rsrc(a.weight, rb);
-        const __amdgpu_buffer_rsrc_t tsc = make_rsrc(a.scale + i * a.ld_scale, rb);
-        const __amdgpu_buffer_rsrc_t tsh = make_rsrc(a.shift + i * a.ld_shift, rb);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = lane + 64 * j;
             const bool in = FULL || c < nchunk;
-            const v4u wv = ld16(tw, c), sc = ld16(tsc, c), sh = ld16(tsh, c);
+            asm volatile("" ::: "memory");            // this chunk's table loads are not hoisted above here
+            const v4u sc = ld16(gsc, c), sh = ld16(gsh, c);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
+                const v4f wf = tabs[T_W][k >> 1][c];
                 float o[2];
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
-                    const float we = u2f(e ? (wv[k] & 0xffff0000u) : (wv[k] << 16));
+                    const float we = wf[2 * (k & 1) + e];
                     const float se = u2f(e ? (sc[k] & 0xffff0000u) : (sc[k] << 16));
                     const float be = u2f(e ? (sh[k] & 0xffff0000u) : (sh[k] << 16));
                     const float n = (xf[j][2 * k + e] * r) * we;
@@ -445,7 +536,6 @@ __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
                 h[j][k] = in ? cvt_bf16x2(o[0], o[1]) : 0u;
                 mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, h[j][k] & 0x7fff7fffu));
             }
-            __builtin_amdgcn_sched_barrier(0);          // one chunk's table loads in flight at a time
         }
     }
     uint32_t mx = (uint32_t)(mx2[0] > mx2[1] ? mx2[0] : mx2[1]) << 16;
@@ -477,13 +567,13 @@ int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
     return H3FP8_OK;
 }
 
-template <int OUT, int CPL>
+template <bool GATE, bool B32, int OUT, int CPL>
 int launch_rms_staged(const RmsArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)((a.M + 7) / 8)), block(512);
     if (a.H == 512 * CPL)
-        hipLaunchKernelGGL((rms_mod_quant_staged_kernel<OUT, CPL, true>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((rms_mod_quant_staged_kernel<GATE, B32, OUT, CPL, true>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((rms_mod_quant_staged_kernel<OUT, CPL, false>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((rms_mod_quant_staged_kernel<GATE, B32, OUT, CPL, false>), grid, block, 0, st, a);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
@@ -491,9 +581,13 @@ int launch_rms_staged(const RmsArgs& a, hipStream_t st) {
 template <bool GATE, int OUT, bool B32 = false>
 int launch_rms(const RmsArgs& a, hipStream_t st) {
     const int64_t cpl = ((a.H >> 3) + 63) / 64;
-    if (!GATE && !B32 && cpl > 2 && cpl <= 4) return launch_rms_staged<OUT, 4>(a, st);
-    if (!GATE && !B32 && cpl > 4 && cpl <= 6) return launch_rms_staged<OUT, 6>(a, st);
-    if (!GATE && !B32 && cpl > 6 && cpl <= 8) return launch_rms_staged<OUT, 8>(a, st);
+    // the staged form for the qkv producer and the out consumer; the fc1 producer (bf16 branch) measured slower
+    // with it (109 -> 121 us at 1344x768: its own HBM stream already fills the time)
+    if constexpr (!GATE || B32) {
+        if (cpl > 2 && cpl <= 4) return launch_rms_staged<GATE, B32, OUT, 4>(a, st);
+        if (cpl > 4 && cpl <= 6) return launch_rms_staged<GATE, B32, OUT, 6>(a, st);
+        if (cpl > 6 && cpl <= 8) return launch_rms_staged<GATE, B32, OUT, 8>(a, st);
+    }
     if (cpl <= 2) return launch_rms_cpl<GATE, OUT, 2, B32>(a, st);
     if (cpl <= 4) return launch_rms_cpl<GATE, OUT, 4, B32>(a, st);
     if (cpl <= 6) return launch_rms_cpl<GATE, OUT, 6, B32>(a, st);

@@ -124,6 +124,47 @@ def test_gate_rms_matches_oracle(cuda, T, hidden, bias):
     assert_quant_equal(q2, s2, q_ref, s_ref)
 
 
+@pytest.mark.parametrize("T,hidden", [(1003, 3072), (45, 2048), (70, 3000), (29, 4096)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_gate_rms_index_runs(cuda, T, hidden, bias):
+    """The out-projection consumer over index runs (one index per sample): 8-row workgroups whose rows share their
+    first row's index read the tables staged in LDS, the ones straddling a run boundary read the other rows' gate /
+    scale / shift from global memory; an index outside the tables at a workgroup's first row and inside one.  Both
+    output forms (residual_out + modulated, residual_out + quant) bit-exact against the oracle on every other row."""
+    from h3_tp2_amd import ops
+    x32, sa, sb, b = _operands(T, hidden, seed=T * 3 + hidden, bias=bias)
+    res, w, sh, sc, gt, _ = mod_inputs(T, hidden, seed=T + 5 * hidden, B=4)
+    runs = [1, 3, 5, 8, 13, 2, 40, 7, 9, 100]
+    vals, k = [], 0
+    while len(vals) < T:
+        vals += [k % 4] * runs[k % len(runs)]
+        k += 1
+    idx = torch.tensor(vals[:T], dtype=torch.int64)
+    bad = idx.clone()
+    poisoned = [m for m in (24, 29) if m < T]
+    for m in poisoned:
+        bad[m] = 4 if m == 24 else -1
+    ok = [m for m in range(T) if m not in poisoned]
+    branch = _epi(x32, sa, sb, b)
+    r_ref, h_ref, q_ref, s_ref = O.gate_rms_quant(bits16(res[ok]), bits16(gt), branch[ok], bits16(w), bits16(sh),
+                                                  bits16(sc), idx[ok].numpy(), EPS)
+    base = sh._base.to(cuda)
+    shd, scd, gd = base[:, :hidden], base[:, hidden:2 * hidden], base[:, 2 * hidden:3 * hidden]
+    x32d, sad, sbd, bd = _dev(x32, sa, sb, b, cuda=cuda)
+    r1, h1 = ops.scale_gate_rms_quant(x32d, sad, sbd, bd, res.to(cuda), gd, w.to(cuda), shd, scd, bad.to(cuda), EPS)
+    r2, q2, s2 = ops.scale_gate_rms_quant(x32d, sad, sbd, bd, res.to(cuda), gd, w.to(cuda), shd, scd, bad.to(cuda),
+                                          EPS, quant=True, modulated=False)
+    torch.cuda.synchronize()
+    for r in (r1, r2):
+        _nan_aware_equal(bits16(r)[ok], r_ref, "residual_out")
+    _nan_aware_equal(bits16(h1)[ok], h_ref, "modulated")
+    qb, sf = q2.view(torch.uint8).cpu(), s2.cpu()
+    assert_quant_equal(qb[ok], sf[ok], q_ref, s_ref)
+    for m in poisoned:
+        assert ((bits16(r1)[m] & 0x7FFF) > 0x7F80).all() and ((bits16(h1)[m] & 0x7FFF) > 0x7F80).all()
+        assert torch.isnan(sf[m]).item() and ((qb[m] & 0x7F) == 0x7F).all()
+
+
 @pytest.mark.parametrize("T,hidden", [(1, 128), (37, 200), (2000, 3072), (3, 8), (65, 5376), (9, 8192)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_indexed_gate_matches_oracle(cuda, T, hidden, bias):
