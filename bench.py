@@ -406,10 +406,16 @@ def main() -> None:
             wn = (1.0 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16)
             ada = torch.randn(6, 6 * H, device=dev, generator=gen).to(torch.bfloat16)
             shp, scp, gtp = ada[:, :H], ada[:, H:2 * H], ada[:, 2 * H:3 * H]
-            idx = torch.randint(0, 6, (Mp,), device=dev, generator=gen)
+            # indices as the model forms them (one per timestep group and modality, so long runs of rows): the
+            # first 540 rows (a conditioning span) on one index, the rest on another; and, for comparison with the
+            # reference's producer probe (scripts/fp8_quant_fuse_probe.py:72), a random index per row
+            idx = torch.zeros(Mp, dtype=torch.int64, device=dev)
+            idx[:540] = 1
+            idx_rand = torch.randint(0, 6, (Mp,), device=dev, generator=gen)
             if gate:
                 br = torch.randn(Mp, H, device=dev, generator=gen).to(torch.bfloat16)
                 fused = lambda: ops.gate_rms_quant(xp, gtp, br, wn, shp, scp, idx, 1e-6)  # noqa: E731
+                fused_r = lambda: ops.gate_rms_quant(xp, gtp, br, wn, shp, scp, idx_rand, 1e-6)  # noqa: E731
 
                 def unfused():
                     _, hh = ops.indexed_gate_rms_norm_scale_shift(xp, gtp, br, wn, shp, scp, idx, 1e-6)
@@ -417,16 +423,22 @@ def main() -> None:
                 nbytes = 7.0 * Mp * H + 4.0 * Mp          # residual, branch, residual_out (bf16) + q + scale
             else:
                 fused = lambda: ops.rms_quant(xp, wn, shp, scp, idx, 1e-6)  # noqa: E731
+                fused_r = lambda: ops.rms_quant(xp, wn, shp, scp, idx_rand, 1e-6)  # noqa: E731
 
                 def unfused():
                     ops.quant_rows(ops.rms_norm_indexed_scale_shift(xp, wn, shp, scp, idx, 1e-6))
                 nbytes = 3.0 * Mp * H + 4.0 * Mp          # x (bf16) + q + scale
             t_f = time_steps(fused, steps, warm) / steps
+            t_r = time_steps(fused_r, steps, warm) / steps
             t_u = time_steps(unfused, steps, warm) / steps
             res[name] = {"ms": round(t_f, 4), "GB/s": round(nbytes / (t_f * 1e-3) / 1e9, 1),
                          "frac_hbm": round(nbytes / (t_f * 1e-3) / 1e9 / PEAK_GBS, 4),
-                         "unfused_ms": round(t_u, 4), "speedup_vs_unfused": round(t_u / t_f, 3)}
-            del xp, ada, idx
+                         "unfused_ms": round(t_u, 4), "speedup_vs_unfused": round(t_u / t_f, 3),
+                         "indices": "runs (rows 0-539 one index, the rest another)",
+                         "random_index_per_row": {"ms": round(t_r, 4),
+                                                  "GB/s": round(nbytes / (t_r * 1e-3) / 1e9, 1),
+                                                  "frac_hbm": round(nbytes / (t_r * 1e-3) / 1e9 / PEAK_GBS, 4)}}
+            del xp, ada, idx, idx_rand
             if gate:
                 del br
         out["producers_fused_quant"] = res
@@ -458,19 +470,29 @@ def main() -> None:
         resid = torch.randn(Mc, H, device=dev, generator=gen).to(torch.bfloat16)
         wn = (1.0 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16)
         ada = torch.randn(6, 6 * H, device=dev, generator=gen).to(torch.bfloat16)
-        idx = torch.randint(0, 6, (Mc,), device=dev, generator=gen)
+        # indices in runs as the model forms them, and a random index per row for comparison (see the producers)
+        idx = torch.zeros(Mc, dtype=torch.int64, device=dev)
+        idx[:540] = 1
+        idx_rand = torch.randint(0, 6, (Mc,), device=dev, generator=gen)
         st = fc.Stash(x32, sa_c, sb_c, None, torch.empty((Mc, H), device=dev, dtype=torch.bfloat16))
         t_out = time_steps(lambda: fc.gate_rms_fused(st, resid, ada[:, 2 * H:3 * H], wn, ada[:, :H], ada[:, H:2 * H],
                                                      idx, 1e-6), steps, warm) / steps
+        t_out_r = time_steps(lambda: fc.gate_rms_fused(st, resid, ada[:, 2 * H:3 * H], wn, ada[:, :H],
+                                                       ada[:, H:2 * H], idx_rand, 1e-6), steps, warm) / steps
         out_bytes = Mc * H * (4.0 + 2 + 2 + 2)                       # product, residual in; residual_out, h out
         t_fc2 = time_steps(lambda: fc.gate_fused(st, resid, ada[:, 5 * H:], idx), steps, warm) / steps
         fc2_bytes = Mc * H * (4.0 + 2 + 2)                           # product, x in; out
         res["out_gate_rms_31248x3072"] = {"ms": round(t_out, 4), "GB/s": round(out_bytes / (t_out * 1e-3) / 1e9, 1),
-                                          "frac_hbm": round(out_bytes / (t_out * 1e-3) / 1e9 / PEAK_GBS, 4)}
+                                          "frac_hbm": round(out_bytes / (t_out * 1e-3) / 1e9 / PEAK_GBS, 4),
+                                          "indices": "runs (rows 0-539 one index, the rest another)",
+                                          "random_index_per_row": {
+                                              "ms": round(t_out_r, 4),
+                                              "GB/s": round(out_bytes / (t_out_r * 1e-3) / 1e9, 1),
+                                              "frac_hbm": round(out_bytes / (t_out_r * 1e-3) / 1e9 / PEAK_GBS, 4)}}
         res["fc2_indexed_gate_31248x3072"] = {"ms": round(t_fc2, 4),
                                               "GB/s": round(fc2_bytes / (t_fc2 * 1e-3) / 1e9, 1),
                                               "frac_hbm": round(fc2_bytes / (t_fc2 * 1e-3) / 1e9 / PEAK_GBS, 4)}
-        del x32, st, resid, ada
+        del x32, st, resid, ada, idx, idx_rand
         out["consumers_of_fp32_product"] = res
 
     # ---- CPU baseline: the reference's torch CPU path of the headline chain on a row sample ----

@@ -79,23 +79,27 @@ def test_quant_exhaustive_row_maximum(cuda):
     assert_quant_equal(q, s, *oracle_quant(h))
 
 
-def test_quant_nonfinite_rows(cuda):
-    """NaN / inf in a row: in the first and in the second half of the row (K = 3072 splits a row over two waves that
-    exchange their maxima), and in a row whose other half holds the largest finite value."""
+@pytest.mark.parametrize("M", [7, 16387])
+def test_quant_nonfinite_rows(cuda, M):
+    """NaN / inf in a row: in the first and in the second half of the row (from 16 384 rows on, K = 3072 splits a row
+    over two waves that exchange their maxima; 16 387 rows leave the last workgroup half empty), and in a row whose
+    other half holds the largest finite value; the same rows again as the last ones."""
     K = 3072
-    x = torch.randn(7, K, generator=torch.Generator().manual_seed(1))
-    x[0, 10] = float("nan")
-    x[1, 20] = float("inf")
-    x[2, 30] = -float("inf")
-    x[4, K - 20] = float("nan")
-    x[5, K - 30] = -float("inf")
-    x[6, 5] = 3.0e38
-    x[6, K - 1] = float("inf")
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(1))
+    for base in sorted({0, M - 7}):
+        x[base + 0, 10] = float("nan")
+        x[base + 1, 20] = float("inf")
+        x[base + 2, 30] = -float("inf")
+        x[base + 4, K - 20] = float("nan")
+        x[base + 5, K - 30] = -float("inf")
+        x[base + 6, 5] = 3.0e38
+        x[base + 6, K - 1] = float("inf")
     x = x.to(BF16)
     q, s = _run(x, cuda)
     assert_quant_equal(q, s, *oracle_quant(x))
-    assert torch.isnan(s[0]).item() and torch.isinf(s[1]).item()
-    assert torch.isnan(s[4]).item() and torch.isinf(s[5]).item() and torch.isinf(s[6]).item()
+    for base in sorted({0, M - 7}):
+        assert torch.isnan(s[base]).item() and torch.isinf(s[base + 1]).item()
+        assert torch.isnan(s[base + 4]).item() and torch.isinf(s[base + 5]).item() and torch.isinf(s[base + 6]).item()
 
 
 def test_quant_strided_rows_and_empty(cuda):
