@@ -136,6 +136,24 @@ def test_grouped_matches_single(cuda):
         assert torch.equal(y.view(torch.int16), _gemm(a, w, sa, sb).view(torch.int16))
 
 
+@pytest.mark.parametrize("shapes", [[(32, 1024, 512), (33, 1024, 512), (1, 256, 4096), (2, 3072, 18432)],
+                                    [(2, 3072, 18432), (17, 1536, 4608)]])
+def test_grouped_small_groups(cuda, shapes):
+    """Groups of at most 32 rows inside the grouped launch (its tiles mostly zero rows) against their single launches,
+    which take the small-M form: bit for bit (the same MFMA sequence per element), integer groups against the oracle
+    too; a list of small groups only, and the 32 / 33 row boundary."""
+    from h3_tp2_amd import ops
+    probs = [serving_like(M, N, K, seed=400 + i, device=cuda) for i, (M, K, N) in enumerate(shapes)]
+    ints = [int_operands(M, N, K, seed=500 + i, device=cuda) for i, (M, K, N) in enumerate(shapes)]
+    outs = ops.grouped_gemm(probs)
+    outs_i = ops.grouped_gemm(ints)
+    torch.cuda.synchronize()
+    for (a, w, sa, sb), y in zip(probs, outs):
+        assert torch.equal(y.view(torch.int16), _gemm(a, w, sa, sb).view(torch.int16))
+    for (a, w, sa, sb), y in zip(ints, outs_i):
+        assert np.array_equal(bits16(y), ref_gemm(a, w, sa, sb))
+
+
 def test_side_stream_and_scaled_mm_layout(cuda):
     from h3_tp2_amd import ops
     a, w, sa, sb = serving_like(1000, 5376, 7168, seed=5, device=cuda)
