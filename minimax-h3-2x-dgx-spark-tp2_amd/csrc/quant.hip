@@ -163,20 +163,16 @@ int launch_quant(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int6
     uint8_t* qp = (uint8_t*)q;
     // Rows of 6 or more chunks per lane go to two waves of half the chunks each: half the registers per wave, twice
     // the waves in flight (measured at M = 91 728: with the maximum given K = 8192 427 -> 383 us, K = 3072
-    // 129.7 -> 127.7 us, four waves of a quarter the same as two; the full quant at K = 3072 128.5 -> 125.0 us).
-    // The full quant keeps one wave per row below 16 384 rows: at M = 16 740 (K = 3072) the two forms measure the
-    // same, and on smaller grids the exchange's barrier has nothing to gain.
+    // 129.7 -> 127.7 us, four waves of a quarter the same as two; the full quant at K = 3072 128.5 -> 125.0 us, and
+    // at M = 2048 / 8192 / 16 740 the same as one wave per row or slightly faster)
 #define H3_Q(N)                                                                                                        \
     do {                                                                                                               \
-        if constexpr (N >= 6) {                                                                                        \
-            if (KNOWN || M >= 16384) {                                                                                 \
-                hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2>), dim3((unsigned)((M + 1) / 2)), block, 0, st,  \
-                                   xp, ldx, M, K, qp, ldq, scale, row_amax);                                           \
-                break;                                                                                                 \
-            }                                                                                                          \
-        }                                                                                                              \
-        hipLaunchKernelGGL((quant_rows_kernel<N, KNOWN>), grid, block, 0, st, xp, ldx, M, K, qp, ldq, scale,           \
-                           row_amax);                                                                                  \
+        if constexpr (N >= 6)                                                                                          \
+            hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2>), dim3((unsigned)((M + 1) / 2)), block, 0, st, xp,  \
+                               ldx, M, K, qp, ldq, scale, row_amax);                                                   \
+        else                                                                                                           \
+            hipLaunchKernelGGL((quant_rows_kernel<N, KNOWN>), grid, block, 0, st, xp, ldx, M, K, qp, ldq, scale,       \
+                               row_amax);                                                                              \
     } while (0)
     if (cpl <= 1) H3_Q(1);
     else if (cpl <= 2) H3_Q(2);

@@ -81,9 +81,9 @@ def test_quant_exhaustive_row_maximum(cuda):
 
 @pytest.mark.parametrize("M", [7, 16387])
 def test_quant_nonfinite_rows(cuda, M):
-    """NaN / inf in a row: in the first and in the second half of the row (from 16 384 rows on, K = 3072 splits a row
-    over two waves that exchange their maxima; 16 387 rows leave the last workgroup half empty), and in a row whose
-    other half holds the largest finite value; the same rows again as the last ones."""
+    """NaN / inf in a row: in the first and in the second half of the row (K = 3072 splits a row over two waves that
+    exchange their maxima; an odd row count leaves the last workgroup half empty), and in a row whose other half holds
+    the largest finite value; the same rows again as the last ones."""
     K = 3072
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(1))
     for base in sorted({0, M - 7}):
