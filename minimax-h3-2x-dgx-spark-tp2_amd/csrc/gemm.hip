@@ -12,8 +12,8 @@
 //   * the MFMA's A operand is the weight tile (rows n) and its B operand the activation tile (rows m), so each group of
 //     four accumulators of a lane holds four consecutive channels n of one token m;
 //   * global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging): each instruction moves 8 rows x 128 bytes, i.e.
-//     whole 128-byte lines (64-byte row pieces halve the load path's throughput: measured 22 vs 40 bytes/clk/CU);
-//     out-of-range rows and the K tail read as zero through the buffer descriptor's range check;
+//     whole 128-byte lines (64-byte row pieces measured at about half the throughput); out-of-range rows and the K
+//     tail read as zero through the buffer descriptor's range check;
 //   * two LDS stages (2 x 64 KiB); a stage is released by a barrier right after the last reads of its k-step (early in
 //     the step), and the loads of k-step i+2 are issued one per MFMA over the following 16 MFMAs (issued in bursts they
 //     stall the instruction stream);
@@ -37,6 +37,9 @@
 // the sign rotated to the lowest bit so that both signs form one contiguous range); a pass of 32 tokens with any gate
 // outside that range (zeros, tinier, larger, inf, NaN -- the wave votes) reads the full table in global memory
 // instead.  Both give the same table entry, so the output does not depend on the path taken.
+// Other forms below, each with the same MFMA sequence per output element (so the same bits): the half-tile kernel
+// (256 tokens x 128 channels, three stages) for a problem's last partial round and for problems of fewer tiles than
+// CUs, and the small-M form (M <= 32: one wave per 32 weight rows, the weight streamed once).
 #include <algorithm>
 
 #include "h3fp8_common.h"
