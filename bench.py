@@ -86,8 +86,8 @@ def profile_traffic(name: str):
 def main() -> None:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs the online-FP8 path on one GPU only (the full token sequence resident, no "
-              "sharding, no collectives); --gpus must be 1", file=sys.stderr)
+        print("bench.py: the online-FP8 path runs on one GPU only (the full token sequence resident, no sharding, no "
+              "collectives); --gpus must be 1", file=sys.stderr)
         sys.exit(2)
     import torch
 
