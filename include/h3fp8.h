@@ -204,6 +204,11 @@ int h3fp8_gate_rms_quant(const void* residual, int64_t ldr, const void* gate, in
  *                               n_d (d >= 96).  out_q [T, Hq, 128] / out_k [T, Hk, 128] with token / head strides.
  *                               The v columns take h3fp8_scale_bias_cast.  Replaces qk_norm_rope_fused /
  *                               _scale_rms_norm_rope_kernel (h3_tp2/fp8_consumers.py:424-461, :131-193).
+ *   h3fp8_scale_qkv_norm_rope   the same with the v columns in the same launch: the Hv heads after the k heads get
+ *                               the scale pass alone, out_v [T, Hv, 128] = bf16(sa (sb acc)) (bias: one fma), the
+ *                               bytes h3fp8_scale_bias_cast writes (Hv = 0: h3fp8_scale_qk_norm_rope).  Replaces
+ *                               qk_norm_rope_fused with its v scale_pass_into (h3_tp2/fp8_consumers.py:424-461,
+ *                               :373-380).
  * Sums of squares as in the producers (fp32 squares, fp64 sum, one rounding).
  */
 int h3fp8_scale_gate_rms_quant(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
@@ -220,6 +225,11 @@ int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, 
                              int64_t T, int Hq, int Hk, const void* q_weight, const void* k_weight, const void* rope,
                              int64_t ld_rope, int rope_f32, float eps, void* out_q, int64_t ldq_t, int64_t ldq_h,
                              void* out_k, int64_t ldk_t, int64_t ldk_h, void* stream);
+int h3fp8_scale_qkv_norm_rope(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                              int64_t T, int Hq, int Hk, int Hv, const void* q_weight, const void* k_weight,
+                              const void* rope, int64_t ld_rope, int rope_f32, float eps, void* out_q, int64_t ldq_t,
+                              int64_t ldq_h, void* out_k, int64_t ldk_t, int64_t ldk_h, void* out_v, int64_t ldv_t,
+                              int64_t ldv_h, void* stream);
 
 /*
  * The two-pass scale pass: y = round(sa[m] * (sb[n] * x32[m, n])) (bias: one fma), bf16 or fp16.

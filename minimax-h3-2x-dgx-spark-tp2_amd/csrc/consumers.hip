@@ -14,9 +14,11 @@
 //
 // A 64-lane wave takes a group of 8 heads of two consecutive tokens: lanes 8j .. 8j + 7 hold head 8g + j, lane k of
 // the eight dims 32i + 4k .. 32i + 4k + 3 for i = 0 .. 3 (16 dims per lane, so the per-head work -- the butterfly, the
-// two divisions, the square root -- is shared by 16 dims), 4 waves per 256-thread workgroup.  The v
-// columns of the product go through the plain scale pass (h3fp8_scale_bias_cast) into the placeholder, where the
-// attention reads them.
+// two divisions, the square root -- is shared by 16 dims), 4 waves per 256-thread workgroup.  The v columns of the
+// product (Hv heads after the k heads) take the plain scale pass into the placeholder, where the attention reads them:
+// in the same launch (h3fp8_scale_qkv_norm_rope: every token pair's v heads are three more groups of 8, each wave
+// x_d = bf16(sa[t] * (sb[c] * acc[t, c])) only, the same lane layout and rounding; 168.5 us against 177-180 us for a
+// second launch at 16 740 tokens) or through h3fp8_scale_bias_cast.
 #include "h3fp8_common.h"
 
 namespace {
@@ -41,6 +43,9 @@ struct QkArgs {
     int64_t ldq_t, ldq_h;
     uint16_t* out_k;            // bf16 [T, Hk, 128]
     int64_t ldk_t, ldk_h;
+    int Hv;                     // v heads after the k heads (0: none): scale pass only
+    uint16_t* out_v;            // bf16 [T, Hv, 128]
+    int64_t ldv_t, ldv_h;
 };
 
 // Sum over the 8 lanes of a head in fp64 (xor butterfly over 4, 2, 1: stays inside each group of 8 lanes).
@@ -201,15 +206,63 @@ __device__ __forceinline__ void qk_compute(const QkArgs& a, const QkIn& L, int l
 // A wave takes head group g of two consecutive tokens: both tokens' loads are issued before either is computed, and
 // the loads that do not depend on the token (sb, bias, norm weights: the same addresses) are issued once.  An odd
 // token count leaves the last wave's second token a copy of its first, not stored.
+// The v heads of two tokens: the scale pass alone (the same lane layout, the same arithmetic and rounding as the q / k
+// heads' scale pass), stored to out_v.
+template <bool HB>
+__device__ __forceinline__ void v_pass(const QkArgs& a, int64_t t0, int64_t t1, bool st1, int gv, int lane) {
+    const int k = lane & 7;
+    const int hv = 8 * gv + (lane >> 3);
+    if (hv >= a.Hv) return;
+    const int64_t c = (int64_t)(a.Hq + a.Hk + hv) * 128 + 4 * k;
+    v4f av[2][4], sv[4];
+    uint2 bw[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float* ap = a.acc + (u ? t1 : t0) * a.ld_acc + c;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) av[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(ap + 32 * i));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = *reinterpret_cast<const v4f*>(a.sb + c + 32 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bw[i] = HB ? *reinterpret_cast<const uint2*>(a.bias + c + 32 * i) : make_uint2(0u, 0u);
+    const float sam[2] = {a.sa[t0], a.sa[t1]};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        if (u == 1 && !st1) break;
+        uint16_t* out = a.out_v + (u ? t1 : t0) * a.ldv_t + (int64_t)hv * a.ldv_h + 4 * k;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p = sv[i][e] * av[u][i][e];
+                if (HB) {
+                    const uint32_t bb = (e >> 1) ? bw[i].y : bw[i].x;
+                    x[e] = __builtin_fmaf(sam[u], p, (e & 1) ? hi_bf16(bb) : lo_bf16(bb));
+                } else {
+                    x[e] = sam[u] * p;
+                }
+            }
+            *reinterpret_cast<uint2*>(out + 32 * i) = make_uint2(cvt_bf16x2(x[0], x[1]), cvt_bf16x2(x[2], x[3]));
+        }
+    }
+}
+
 template <bool HB, bool RF>
 __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64_t units) {
     const int lane = threadIdx.x & 63;
-    const int groups = (a.Hq + a.Hk + 7) / 8;
+    const int qk_groups = (a.Hq + a.Hk + 7) / 8;
+    const int groups = qk_groups + (a.Hv + 7) / 8;
     const int64_t w = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (w >= units) return;
     const int64_t tp = w / groups;
     const int g = (int)(w - tp * groups);
     const int64_t t0 = 2 * tp, t1 = t0 + 1 < a.T ? t0 + 1 : t0;
+    if (g >= qk_groups) {
+        v_pass<HB>(a, t0, t1, t0 + 1 < a.T, g - qk_groups, lane);
+        return;
+    }
     QkIn L0, L1;
     qk_load<HB, RF>(a, t0, g, lane, L0);
     qk_load<HB, RF>(a, t1, g, lane, L1);
@@ -221,15 +274,19 @@ __global__ void __launch_bounds__(256) scale_qk_norm_rope_kernel(QkArgs a, int64
 
 extern "C" {
 
-int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
-                             int64_t T, int Hq, int Hk, const void* q_weight, const void* k_weight, const void* rope,
-                             int64_t ld_rope, int rope_f32, float eps, void* out_q, int64_t ldq_t, int64_t ldq_h,
-                             void* out_k, int64_t ldk_t, int64_t ldk_h, void* stream) {
-    H3_REQUIRE(T >= 0 && Hq >= 0 && Hk >= 0, "h3fp8_scale_qk_norm_rope: negative size");
-    if (T == 0 || Hq + Hk == 0) return H3FP8_OK;
+int h3fp8_scale_qkv_norm_rope(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                              int64_t T, int Hq, int Hk, int Hv, const void* q_weight, const void* k_weight,
+                              const void* rope, int64_t ld_rope, int rope_f32, float eps, void* out_q, int64_t ldq_t,
+                              int64_t ldq_h, void* out_k, int64_t ldk_t, int64_t ldk_h, void* out_v, int64_t ldv_t,
+                              int64_t ldv_h, void* stream) {
+    H3_REQUIRE(T >= 0 && Hq >= 0 && Hk >= 0 && Hv >= 0, "h3fp8_scale_qk_norm_rope: negative size");
+    if (T == 0 || Hq + Hk + Hv == 0) return H3FP8_OK;
+    H3_REQUIRE(Hv == 0 || (out_v && ((uintptr_t)out_v & 7) == 0 && ldv_t % 4 == 0 && ldv_h % 4 == 0 && ldv_h >= 128),
+               "h3fp8_scale_qkv_norm_rope: the v output needs 8-byte alignment and strides that are multiples of 4, "
+               "dims contiguous");
     H3_REQUIRE(acc && sa && sb && q_weight && k_weight && rope && (Hq == 0 || out_q) && (Hk == 0 || out_k),
                "h3fp8_scale_qk_norm_rope: null pointer");
-    H3_REQUIRE(ld_acc >= (int64_t)(Hq + Hk) * 128 && ld_acc % 4 == 0 && ((uintptr_t)acc & 15) == 0 &&
+    H3_REQUIRE(ld_acc >= (int64_t)(Hq + Hk + Hv) * 128 && ld_acc % 4 == 0 && ((uintptr_t)acc & 15) == 0 &&
                    ((uintptr_t)sb & 15) == 0 && ((uintptr_t)bias & 7) == 0,
                "h3fp8_scale_qk_norm_rope: the product needs 16-byte aligned rows (stride >= (Hq + Hk) * 128, a "
                "multiple of 4), sb 16-byte and bias 8-byte alignment");
@@ -249,7 +306,8 @@ int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, 
     a.rope = rope; a.ld_rope = ld_rope; a.rope_f32 = rope_f32 ? 1 : 0; a.eps = eps;
     a.out_q = (uint16_t*)out_q; a.ldq_t = ldq_t; a.ldq_h = ldq_h;
     a.out_k = (uint16_t*)out_k; a.ldk_t = ldk_t; a.ldk_h = ldk_h;
-    const int64_t units = ((T + 1) / 2) * ((Hq + Hk + 7) / 8);
+    a.Hv = Hv; a.out_v = (uint16_t*)out_v; a.ldv_t = ldv_t; a.ldv_h = ldv_h;
+    const int64_t units = ((T + 1) / 2) * ((Hq + Hk + 7) / 8 + (Hv + 7) / 8);
     H3_REQUIRE(units < ((int64_t)1 << 33), "h3fp8_scale_qk_norm_rope: too many tokens");
     const dim3 grid((unsigned)((units + 3) / 4)), block(256);
     hipStream_t st = (hipStream_t)stream;
@@ -259,6 +317,14 @@ int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, 
     else hipLaunchKernelGGL((scale_qk_norm_rope_kernel<false, false>), grid, block, 0, st, a, units);
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
+}
+
+int h3fp8_scale_qk_norm_rope(const float* acc, int64_t ld_acc, const float* sa, const float* sb, const void* bias,
+                             int64_t T, int Hq, int Hk, const void* q_weight, const void* k_weight, const void* rope,
+                             int64_t ld_rope, int rope_f32, float eps, void* out_q, int64_t ldq_t, int64_t ldq_h,
+                             void* out_k, int64_t ldk_t, int64_t ldk_h, void* stream) {
+    return h3fp8_scale_qkv_norm_rope(acc, ld_acc, sa, sb, bias, T, Hq, Hk, 0, q_weight, k_weight, rope, ld_rope,
+                                     rope_f32, eps, out_q, ldq_t, ldq_h, out_k, ldk_t, ldk_h, nullptr, 0, 0, stream);
 }
 
 }  // extern "C"

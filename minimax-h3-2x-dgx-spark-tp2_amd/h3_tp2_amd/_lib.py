@@ -57,6 +57,8 @@ _SIGS = {
     "h3fp8_scale_indexed_gate": ([P, I64, P, P, P, P, I64, P, I64, I64, P, I64, I, I64, I64, P, I64, P], I),
     "h3fp8_scale_qk_norm_rope": ([P, I64, P, P, P, I64, I, I, P, P, P, I64, I, ctypes.c_float, P, I64, I64, P, I64,
                                   I64, P], I),
+    "h3fp8_scale_qkv_norm_rope": ([P, I64, P, P, P, I64, I, I, I, P, P, P, I64, I, ctypes.c_float, P, I64, I64, P,
+                                   I64, I64, P, I64, I64, P], I),
     "h3fp8_scale_bias_cast": ([P, I64, P, I64, P, I64, P, P, I64, I, I64, I64, P], I),
     "h3fp8_grouped_gemm": ([ctypes.POINTER(Group), I, P], I),
     "h3fp8_selfcheck_e4m3": ([ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], I),

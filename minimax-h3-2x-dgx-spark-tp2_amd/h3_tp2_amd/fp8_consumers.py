@@ -199,12 +199,18 @@ def qk_norm_rope_fused(st: Stash, num_heads: int, num_kv_heads: int, head_dim: i
     x32, sa, sb, bias, ph = st.x32, st.sa, st.sb, st.bias, st.ph
     T = x32.shape[0]
     v0 = (num_heads + num_kv_heads) * head_dim
+    v = ph[:, v0:].view(T, num_kv_heads, head_dim)
+    if T and head_dim == 128 and x32.shape[1] == v0 + num_kv_heads * head_dim:
+        # q, k and the v columns' scale pass in one launch
+        oq, ok = ops.scale_qk_norm_rope(x32, sa, sb, bias, num_heads, num_kv_heads, q_weight.contiguous(),
+                                        k_weight.contiguous(), rope_table, eps, v_out=v)
+        return oq, ok, v
     oq, ok = ops.scale_qk_norm_rope(x32, sa, sb, bias, num_heads, num_kv_heads, q_weight.contiguous(),
                                     k_weight.contiguous(), rope_table, eps)
     if T:
         ops.scale_bias_cast(x32[:, v0:], sa, sb[v0:], None if bias is None else bias[v0:], torch.bfloat16,
                             out=ph[:, v0:])
-    return oq, ok, ph[:, v0:].view(T, num_kv_heads, head_dim)
+    return oq, ok, v
 
 
 def gate_rms_fused(st: Stash, residual: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, shift: torch.Tensor,

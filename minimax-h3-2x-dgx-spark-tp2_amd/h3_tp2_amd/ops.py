@@ -473,12 +473,20 @@ def scale_indexed_gate(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bi
 
 def scale_qk_norm_rope(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None,
                        num_heads: int, num_kv_heads: int, q_weight: torch.Tensor, k_weight: torch.Tensor,
-                       rope_table: torch.Tensor, eps: float):
+                       rope_table: torch.Tensor, eps: float, v_out: torch.Tensor | None = None):
     """q, k of ``fused_qk_norm_rope`` (head_dim 128, rotary 96, half-split) on the qkv GEMM's fp32 product: the q heads
     are product columns [0, 128 H), the k heads the next 128 Hk.  Returns (q [T, H, 128], k [T, Hk, 128]) bf16
-    (h3_tp2/fp8_consumers.py:424-461 without the v pass)."""
+    (h3_tp2/fp8_consumers.py:424-461).  With ``v_out`` (bf16 [T, Hv, 128], dims contiguous) the Hv heads after the k
+    heads get the scale pass into it in the same launch, the bytes ``scale_bias_cast`` writes
+    (h3_tp2/fp8_consumers.py:373-380)."""
     T = x32.shape[0]
-    s_a, s_b = _product_args(x32, sa, sb, bias, T, (num_heads + num_kv_heads) * 128)
+    Hv = 0
+    if v_out is not None:
+        if v_out.dtype != torch.bfloat16 or v_out.dim() != 3 or v_out.shape[0] != T or v_out.shape[2] != 128 \
+                or v_out.stride(2) != 1 or v_out.device != x32.device:
+            raise ValueError(f"v_out must be bf16 [{T}, Hv, 128] on the product's device with contiguous dims")
+        Hv = v_out.shape[1]
+    s_a, s_b = _product_args(x32, sa, sb, bias, T, (num_heads + num_kv_heads + Hv) * 128)
     _need_cuda(q_weight, k_weight, rope_table)
     if rope_table.dim() != 2 or rope_table.shape != (T, 96) or rope_table.stride(1) != 1 \
             or rope_table.dtype not in (torch.float32, torch.bfloat16):
@@ -488,11 +496,12 @@ def scale_qk_norm_rope(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bi
             raise ValueError("q/k norm weights must be contiguous bf16 [128]")
     oq = torch.empty((T, num_heads, 128), device=x32.device, dtype=torch.bfloat16)
     ok = torch.empty((T, num_kv_heads, 128), device=x32.device, dtype=torch.bfloat16)
-    _lib.call("h3fp8_scale_qk_norm_rope", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), s_b.data_ptr(),
-              bias.data_ptr() if bias is not None else None, T, num_heads, num_kv_heads, q_weight.data_ptr(),
+    _lib.call("h3fp8_scale_qkv_norm_rope", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), s_b.data_ptr(),
+              bias.data_ptr() if bias is not None else None, T, num_heads, num_kv_heads, Hv, q_weight.data_ptr(),
               k_weight.data_ptr(), rope_table.data_ptr(), rope_table.stride(0) if T > 1 else 96,
               int(rope_table.dtype == torch.float32), float(eps), oq.data_ptr(), oq.stride(0), oq.stride(1),
-              ok.data_ptr(), ok.stride(0), ok.stride(1), _stream(x32))
+              ok.data_ptr(), ok.stride(0), ok.stride(1), v_out.data_ptr() if Hv else None,
+              v_out.stride(0) if Hv else 0, v_out.stride(1) if Hv else 0, _stream(x32))
     return oq, ok
 
 

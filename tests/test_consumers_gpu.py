@@ -70,6 +70,42 @@ def test_qk_norm_rope_matches_oracle(cuda, T, H, Hk, bias, rope_dtype):
     assert v.data_ptr() == st.ph.data_ptr() + (H + Hk) * D * 2
 
 
+@pytest.mark.parametrize("T", [1, 5, 64])
+@pytest.mark.parametrize("H,Hk,Hv", [(1, 1, 1), (3, 1, 5), (8, 8, 9)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_qkv_one_launch_strided_v(cuda, T, H, Hk, Hv, bias):
+    """q, k and v in one launch: q and k equal the q / k launch's, v (into a padded [T, Hv, 128] buffer, head stride
+    136, token stride Hv * 136 + 8) equals the scale pass's bytes and the oracle's, and nothing outside v's rows is
+    written.  The product has one extra column group past v (ld_acc > (H + Hk + Hv) * 128)."""
+    from h3_tp2_amd import ops
+    D = 128
+    N = (H + Hk + Hv) * D
+    x32, sa, sb, b = _operands(T, N + 16, seed=T * 3 + Hv, bias=bias)
+    g = torch.Generator().manual_seed(8)
+    wq = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    wk = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    rope = rope_table(T, torch.float32)
+    x32d, sad, sbd, bd, wqd, wkd, roped = _dev(x32, sa, sb, b, wq, wk, rope, cuda=cuda)
+    ldh, ldt = 136, Hv * 136 + 8
+    buf = torch.full((T * ldt + 64,), 7.0, dtype=BF16, device=cuda)
+    v = buf.as_strided((T, Hv, D), (ldt, ldh, 1))
+    oq, ok = ops.scale_qk_norm_rope(x32d, sad, sbd, bd, H, Hk, wqd, wkd, roped, EPS, v_out=v)
+    oq2, ok2 = ops.scale_qk_norm_rope(x32d, sad, sbd, bd, H, Hk, wqd, wkd, roped, EPS)
+    v2 = ops.scale_bias_cast(x32d[:, (H + Hk) * D:N], sad, sbd[(H + Hk) * D:N],
+                             None if bd is None else bd[(H + Hk) * D:N], BF16)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(oq), bits16(oq2)) and np.array_equal(bits16(ok), bits16(ok2))
+    assert np.array_equal(bits16(v), bits16(v2).reshape(T, Hv, D))
+    p = _epi(x32, sa, sb, b)
+    assert np.array_equal(bits16(v), p[:, (H + Hk) * D:N].reshape(T, Hv, D))
+    # the padding between heads and tokens and the guard after the buffer keep their sentinel
+    full = buf[:T * ldt].view(T, ldt).cpu().float()
+    mask = torch.ones(T, ldt, dtype=torch.bool)
+    for h in range(Hv):
+        mask[:, h * ldh:h * ldh + D] = False
+    assert bool((full[mask] == 7.0).all()) and bool((buf[T * ldt:] == 7.0).all())
+
+
 def test_qk_norm_rope_sum_order(cuda):
     """A head whose fp32 sum of squares depends on the reduction order (tests/_util.py): as a q and a k head, with
     and without a rotation, the kernel's output equals the oracle's, whose order the CPU suite pins."""
