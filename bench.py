@@ -387,7 +387,7 @@ def main() -> None:
         out["c5_grouped_one_launch"]["adaLN_M2_alone"] = {
             "ms": round(t2, 4), "GB/s": round(wbytes / (t2 * 1e-3) / 1e9, 1),
             "frac_hbm": round(wbytes / (t2 * 1e-3) / 1e9 / PEAK_GBS, 4),
-            "form": f"kernel 2's small-M form on [{Mg},{Kg}] x [{Ng},{Kg}]: {Ng // 32} waves of 32 weight rows, "
+            "form": f"kernel 2's small-M form on [{Mg},{Kg}] x [{Ng},{Kg}]: {Ng // 16} waves of 16 weight rows, "
                     "the weight streamed once (output bitwise the tiled kernel's)"}
         del probs, xs
 

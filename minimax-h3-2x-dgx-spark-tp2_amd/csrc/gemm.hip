@@ -39,7 +39,7 @@
 // instead.  Both give the same table entry, so the output does not depend on the path taken.
 // Other forms below, each with the same MFMA sequence per output element (so the same bits): the half-tile kernel
 // (256 tokens x 128 channels, three stages) for a problem's last partial round and for problems of fewer tiles than
-// CUs, and the small-M form (M <= 32: one wave per 32 weight rows, the weight streamed once).
+// CUs, and the small-M form (M <= 32: one wave per 16 weight rows, the weight streamed once).
 #include <algorithm>
 
 #include "h3fp8_common.h"
@@ -841,29 +841,28 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
 // ---- the small-M form: at most 32 token rows ----
 // With M <= 32 a GEMM is bound by reading its fp8 weight once (the adaLN modulation: M = 2, 18 432 x 3072 = 56.6 MB),
 // and the 256 x 256 tiles above would spend their k-loop on zero token rows with one tile per 256 weight rows.  Here
-// one wavefront (a workgroup of its own) owns 32 weight rows (one MFMA A block) and all the token rows (one MFMA B
-// block, rows past M read as zeros) and streams its k-steps through a private ring of LDS stages with the LDS-DMA
-// loads of the tiled kernel (whole 128-byte lines, 8 rows per instruction), depth - 1 k-steps ahead of the MFMAs.  A
-// stage holds the 32 weight rows and MB 8-row groups of token rows (MB = 1 for M <= 8, else 4; the lanes of token
-// rows past 8 MB take zero operands), and the ring is as deep as 24 KiB allows (4 stages for MB = 1, 3 for MB = 4),
-// so six waves fit a CU (measured at M = 2, N = 18 432, K = 3072: 24 KiB 11.4 us, 32 KiB 11.7 us, 48 KiB 12.0 us;
-// the k-steps in flight are not what bounds it).  No other wave reads the ring, so no barrier: the wave's own vmcnt wait publishes a stage
-// and its own lgkmcnt wait releases it.
+// one wavefront (a workgroup of its own) owns 16 weight rows and all the token rows (one MFMA B block, rows past M read
+// as zeros) and streams its k-steps through a private ring of LDS stages with the LDS-DMA loads of the tiled kernel
+// (whole 128-byte lines, 8 rows per instruction), depth - 1 k-steps ahead of the MFMAs.  The MFMA's A block is 32
+// rows: rows 16-31 repeat rows 0-15 and their results are not stored (a row's result depends on its own A row only).
+// Each wave streams its weight rows at a rate bounded by its own load latency, so more, smaller waves finish sooner:
+// 16 rows per wave against 32 measured M = 2, N = 18 432, K = 3072: 11.0 -> 10.6 us; M = 5: 6.6 -> 5.8 us; M = 17:
+// 4.8 -> 4.4 us; M = 32, K = 8192: 13.9 -> 12.0 us (8 rows per wave: between the two).  A stage holds the 16 weight
+// rows and MB 8-row groups of token rows (MB = 1 for M <= 8, else 4; the lanes of token rows past 8 MB take zero
+// operands); the ring is 4 stages deep for MB = 1 and 3 for MB = 4 (12 / 18 KiB).  No other wave reads the ring, so no
+// barrier: the wave's own vmcnt wait publishes a stage and its own lgkmcnt wait releases it.
 // Every output element goes through the same MFMA sequence as in gemm_kernel: v_mfma 32x32x64 with the weight row at
 // A-row n % 32 and the token at B-column m % 32, the 64-deep k chunks in ascending order, two per 128-deep k-step (a
 // chunk at or past K reads zeros, as the big tiles' last k-step does), and the same epilogue, so the output is bitwise
 // the big kernel's.
 constexpr int ROWS_MAX_M = 32;
-#ifndef H3_ROWS_RING_KIB
-#define H3_ROWS_RING_KIB 24
-#endif
-constexpr int ROWS_RING_BYTES = H3_ROWS_RING_KIB * 1024;
+constexpr int ROWS_RW = 16;                               // weight rows per wave
 
 template <int MB>
 struct RowsRing {
-    static constexpr int STAGE = (32 + 8 * MB) * ROWB;    // 32 weight rows, then 8 MB token rows
-    static constexpr int DEPTH = ROWS_RING_BYTES / STAGE;
-    static constexpr int LOADS = 4 + MB;                  // LDS-DMA instructions per k-step
+    static constexpr int STAGE = (ROWS_RW + 8 * MB) * ROWB;    // the weight rows, then 8 MB token rows
+    static constexpr int DEPTH = MB == 1 ? 4 : 3;
+    static constexpr int LOADS = ROWS_RW / 8 + MB;             // LDS-DMA instructions per k-step
     static_assert(DEPTH >= 2 && LOADS * (DEPTH - 1) <= 63, "vmcnt range");
 };
 
@@ -874,7 +873,7 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[ROWS_DEPTH * ROWS_STAGE];
     const int lane = threadIdx.x;
     const int r = lane & 31, h = lane >> 5;
-    const int n0 = (int)blockIdx.x * 32;
+    const int n0 = (int)blockIdx.x * ROWS_RW;
     const uint32_t lds0 = lds_addr(lds);
     const v4u dw = buffer_desc(p.w, p.w_bytes);
     const v4u da = buffer_desc(p.a, p.a_bytes);
@@ -883,6 +882,7 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
     const int lrow = lane >> 3;
     const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz(lrow)), (uint32_t)((lane & 7) ^ swz(lrow + 8))};
     uint32_t wrow[4], arow[4];                            // byte offsets of this lane's row in each 8-row group
+                                                          // (weights: the first ROWS_RW / 8 groups)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int n = n0 + 8 * i + lrow, m = 8 * i + lrow;
@@ -897,17 +897,19 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
         for (int i = 0; i < 4; ++i) {
             const uint32_t c = (uint32_t)ks * BK + 16u * lch[i & 1];
             const bool in = c < (uint32_t)p.K;
-            dma16(dw, st + (uint32_t)i * 8 * ROWB, in && wrow[i] != OOB ? wrow[i] + c : OOB);
-            if (i < MB) dma16(da, st + 32 * ROWB + (uint32_t)i * 8 * ROWB, in && arow[i] != OOB ? arow[i] + c : OOB);
+            if (i < ROWS_RW / 8) dma16(dw, st + (uint32_t)i * 8 * ROWB, in && wrow[i] != OOB ? wrow[i] + c : OOB);
+            if (i < MB)
+                dma16(da, st + ROWS_RW * ROWB + (uint32_t)i * 8 * ROWB, in && arow[i] != OOB ? arow[i] + c : OOB);
         }
     };
     auto kstep_mfma = [&](v16f& acc, int slot) {
         const uint8_t* st = lds + slot * ROWS_STAGE;
-        const v8i a0 = read_frag(st, lane, 0), a1 = read_frag(st, lane, 1);
+        const int alane = (r % ROWS_RW) | (lane & 32);    // A rows past ROWS_RW repeat rows r % ROWS_RW
+        const v8i a0 = read_frag(st, alane, 0), a1 = read_frag(st, alane, 1);
         v8i b0 = {0, 0, 0, 0, 0, 0, 0, 0}, b1 = b0;
         if (MB == 4 || r < 8 * MB) {                    // token rows past 8 MB: zero operands, nothing staged
-            b0 = read_frag(st + 32 * ROWB, lane, 0);
-            b1 = read_frag(st + 32 * ROWB, lane, 1);
+            b0 = read_frag(st + ROWS_RW * ROWB, lane, 0);
+            b1 = read_frag(st + ROWS_RW * ROWB, lane, 1);
         }
         wait_lgkm0();                                   // the slot is read: the next issue may refill it
         acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a0, b0, acc, 0, 0, 0, 0, 0, 0);
@@ -941,7 +943,8 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
     }
     wait_vm0();                                         // the out-of-range tail loads have landed before the exit
 
-    // epilogue: register 4q + rr holds weight row n0 + 8q + 4h + rr for token r (the MFMA result layout)
+    // epilogue: register 4q + rr holds weight row n0 + 8q + 4h + rr for token r (the MFMA result layout); rows at or
+    // past ROWS_RW are the repeated ones
     const int m = r;
     const bool mok = m < p.M;
     const float sam = mok ? p.sa[(int64_t)m * p.sa_stride] : 0.f;
@@ -949,7 +952,7 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int n = n0 + 8 * q + 4 * h;               // N % 16 == 0: a group of four is wholly in or out
-        if (!mok || n >= p.N) continue;
+        if (8 * q + 4 * h >= ROWS_RW || !mok || n >= p.N) continue;
         if (OUT_DT == H3FP8_DT_F32) {
             const v4f v = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
             *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.y) + (int64_t)m * p.ldy + n) = v;
@@ -982,7 +985,7 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
 
 template <int OUT_DT, bool HAS_BIAS, bool AMAX>
 int launch_rows_t(const GemmParams& p, hipStream_t st) {
-    const dim3 grid((unsigned)((p.N + 31) / 32));
+    const dim3 grid((unsigned)((p.N + ROWS_RW - 1) / ROWS_RW));
     if (p.M <= 8) hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 1>), grid, dim3(64), 0, st, p);
     else hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 4>), grid, dim3(64), 0, st, p);
     H3_CHECK_HIP(hipGetLastError());
@@ -1433,7 +1436,7 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
              int out_dt, int64_t M, int64_t N, int64_t K, int64_t w_rows, float* row_amax, const uint16_t* silu,
              hipStream_t st) {
     if (epi != EPI_SWIGLU && M <= ROWS_MAX_M) {
-        // weight-bound: one wave per 32 weight rows (gemm_rows_kernel), bitwise the tiled kernel's output
+        // weight-bound: one wave per 16 weight rows (gemm_rows_kernel), bitwise the tiled kernel's output
         const GemmParams p = make_params(a, lda, w, ldw, sa, sa_stride, sb, sb_stride, bias, y, ldy, M, N, K, w_rows,
                                          row_amax, silu, false);
         return launch_rows(p, epi, out_dt, bias != nullptr, st);

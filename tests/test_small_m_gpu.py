@@ -1,4 +1,4 @@
-"""The small-M form of kernel 2 (M <= 32 token rows: one wave per 32 weight rows, the weight streamed through a private
+"""The small-M form of kernel 2 (M <= 32 token rows: one wave per 16 weight rows, the weight streamed through a private
 LDS ring).
 
 * Bit-identity with the tiled kernel: the same MFMA sequence per output element (weight row at A-row n % 32, token at
