@@ -323,7 +323,7 @@ def main() -> None:
         out["c1_single_linear_2048x3072x3072"] = {
             "ms": round(t, 4), "TFLOP/s": round(2.0 * M1 * N1 * K1 / (t * 1e-3) / 1e12, 1),
             "frac_mfma": round(2.0 * M1 * N1 * K1 / (t * 1e-3) / 1e12 / PEAK_TFLOPS, 4),
-            "form": "kernel 1 + kernel 2 as 192 half tiles (256 x 128, three stages) on 192 of the 256 CUs"}
+            "form": "kernel 1 + kernel 2 as 256 tiles of 128 tokens x 192 weight rows, one per CU"}
         del x1, w1, q1, y1
 
     if want("c3"):

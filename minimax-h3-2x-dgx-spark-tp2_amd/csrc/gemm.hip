@@ -1173,26 +1173,24 @@ __device__ __forceinline__ void h3s_kstep(uint8_t* lds, uint32_t lds0, int s0, c
     }
 }
 
-// Epilogue of a half tile straight from the accumulators (no LDS staging): register 4q + r of MFMA tile (i, j) is
-// channel col0 + 32 i + 8 q + 4 (lane >> 5) + r of token mrow0 + 32 j + (lane & 31); each lane stores its 4
-// consecutive channels (8 bytes, 16 contiguous bytes with the partner lane l ^ 32).  Rows past M fall outside the
-// output descriptor's range, columns past N get an out-of-range offset.
-template <int OUT_DT, bool HAS_BIAS, int EPI>
-__device__ __forceinline__ void h3s_epilogue(const GemmParams& p, int tm, int tn, const uint8_t* lds, int set, int wn,
-                                             int wm, int lane, v16f acc[4][4]) {
+// Epilogue of a wave's NI x NJ MFMA blocks straight from the accumulators (no LDS staging): register 4q + r of block
+// (i, j) is channel col0 + 32 i + 8 q + 4 (lane >> 5) + r of token mrow0 + 32 j + (lane & 31); sa_l[sa0 + t] and
+// sb_l[sb0 + c] (LDS) hold the scales of token mrow0 + t and channel col0 + c.  Each lane stores its 4 consecutive channels (8 bytes, 16
+// contiguous bytes with the partner lane l ^ 32).  Rows past M fall outside the output descriptor's range, columns past
+// N get an out-of-range offset.
+template <int OUT_DT, bool HAS_BIAS, int EPI, int NI, int NJ, int AI, int AJ>
+__device__ __forceinline__ void reg_epilogue(const GemmParams& p, int col0, int mrow0, const float* sa_l, int sa0,
+                                             const float* sb_l, int sb0, int lane, v16f (&acc)[AI][AJ]) {
+    static_assert(NI <= AI && NJ <= AJ, "blocks of the accumulator array");
     const int hi = lane >> 5, mj = lane & 31;
-    const int col0 = tn * (BN / 2) + wn * 64;
-    const int mrow0 = tm * BM + wm * 128;
-    const float* sa_l = reinterpret_cast<const float*>(lds + H3S_SCALES_OFF + set * SCALE_SET);
-    const float* sb_l = sa_l + 256;
     if (OUT_DT == H3FP8_DT_F32) {
         float* yf = reinterpret_cast<float*>(p.y);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < NJ; ++j) {
                     const int n = col0 + 32 * i + 8 * q + 4 * hi;
                     const int m = mrow0 + 32 * j + mj;
                     if (n < p.N && m < p.M) {
@@ -1206,16 +1204,16 @@ __device__ __forceinline__ void h3s_epilogue(const GemmParams& p, int tm, int tn
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(p.y, p.y_bytes);
     const uint32_t row2 = (uint32_t)p.ldy * 2u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int m = mrow0 + 32 * j + mj;
-        const float sam = sa_l[wm * 128 + 32 * j + mj];
+        const float sam = sa_l[sa0 + 32 * j + mj];
         uint32_t rmax = 0;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int n = col0 + 32 * i + 8 * q + 4 * hi;
-                const v4f sbn = *reinterpret_cast<const v4f*>(sb_l + wn * 64 + 32 * i + 8 * q + 4 * hi);
+                const v4f sbn = *reinterpret_cast<const v4f*>(sb_l + sb0 + 32 * i + 8 * q + 4 * hi);
                 float bn[4] = {0, 0, 0, 0};
                 if (HAS_BIAS) {
                     const int nc = n < p.N ? n : 0;
@@ -1249,6 +1247,16 @@ __device__ __forceinline__ void h3s_epilogue(const GemmParams& p, int tm, int tn
             if (hi == 0 && m < p.M && rmax) atomicMax(reinterpret_cast<unsigned int*>(p.row_amax) + m, rmax);
         }
     }
+}
+
+// A half tile's wave owns 2 x 4 blocks: channels tn * 128 + 64 wn onwards, tokens tm * 256 + 128 wm onwards.
+template <int OUT_DT, bool HAS_BIAS, int EPI>
+__device__ __forceinline__ void h3s_epilogue(const GemmParams& p, int tm, int tn, const uint8_t* lds, int set, int wn,
+                                             int wm, int lane, v16f (&acc)[4][4]) {
+    const float* sa_l = reinterpret_cast<const float*>(lds + H3S_SCALES_OFF + set * SCALE_SET);
+    const float* sb_l = sa_l + 256;
+    reg_epilogue<OUT_DT, HAS_BIAS, EPI, 2, 4>(p, tn * (BN / 2) + wn * 64, tm * BM + wm * 128, sa_l, wm * 128, sb_l,
+                                              wn * 64, lane, acc);
 }
 
 template <int OUT_DT, bool HAS_BIAS, int EPI>
@@ -1305,6 +1313,185 @@ __global__ void __launch_bounds__(256, 1) gemm_half3_kernel(GroupedParams gp) {
     wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
 }
 
+// ---- 128 x 192 tiles, one per workgroup (problems that fit one round) ----
+// A problem whose 256 x 256 tiles number at most half the CUs runs as half tiles, which can still leave CUs idle: the
+// single linear 2048 x 3072 x 3072 has 96 full tiles, 192 half tiles, on 256 CUs.  Tiles of 128 token rows x 192
+// weight rows cover it with 16 x 16 = 256 workgroups, one per CU, each loading 40 KiB per k-step (half tiles: 48).
+// The four waves own 96 weight rows x 64 token rows each (3 x 2 MFMA blocks).  Every output element gets the same
+// MFMA sequence as in the other forms (k sub-steps of 64 in order from a zero accumulator), so the same bits.
+constexpr int W192_WR = 192;                            // weight rows per tile
+constexpr int W192_TR = 128;                            // token rows per tile
+constexpr int W192_STAGE = (W192_WR + W192_TR) * ROWB;  // 40 KiB
+constexpr int W192_A = W192_WR * ROWB;                  // token rows start after the weight rows
+constexpr int W192_NSTAGE = 3;
+constexpr int W192_SCALES_OFF = W192_NSTAGE * W192_STAGE;
+constexpr int W192_JUNK_OFF = W192_SCALES_OFF + SCALE_SET;
+constexpr int W192_LDS = W192_JUNK_OFF + 512;
+static_assert(W192_LDS <= 160 * 1024, "LDS of one CU");
+constexpr int W192_LOADS = 12;                          // per wave and k-step: 6 weight + 4 token + 2 scale loads
+
+struct W192Loader {
+    v4u rw, ra, rsa, rsb;
+    uint32_t vw[2], va[2], vw_t[2], va_t[2];            // lane parts (even / odd 8-row groups); _t: the K-tail k-step
+    uint32_t row8_w, row8_a;
+    uint32_t sa_off, sb_off;
+    uint32_t dsa, dsb;                                  // this wave's share of the tile's scale set (junk when unused)
+    int wgroups, agroups;                               // this wave's 8-row groups that start inside N / M
+    int nk;
+};
+
+// Wave w loads weight rows 48 w .. 48 w + 47 and token rows 32 w .. 32 w + 31 of the tile (6 and 4 groups of 8 rows);
+// waves 0, 1 the sa of the tile's 128 token rows, waves 0..2 the sb of its 192 weight rows.
+__device__ __forceinline__ void w192_loader_set(W192Loader& L, const GemmParams& p, int tm, int tn, uint32_t lds0,
+                                                int wave, int lane) {
+    L.nk = (p.K + BK - 1) / BK;
+    const uint32_t lrow = (uint32_t)(lane >> 3);
+    const uint32_t lch[2] = {(uint32_t)((lane & 7) ^ swz((int)lrow)), (uint32_t)((lane & 7) ^ swz((int)lrow + 8))};
+    const int64_t wrow0 = (int64_t)tn * W192_WR + 48 * wave;
+    const int64_t arow0 = (int64_t)tm * W192_TR + 32 * wave;
+    const int64_t wg = wrow0 < p.N ? (p.N - wrow0 + 7) / 8 : 0, ag = arow0 < p.M ? (p.M - arow0 + 7) / 8 : 0;
+    L.wgroups = (int)(wg < 6 ? wg : 6);
+    L.agroups = (int)(ag < 4 ? ag : 4);
+    L.rw = buffer_desc(p.w, p.w_bytes);
+    L.ra = buffer_desc(p.a, p.a_bytes);
+    const uint32_t ktail = (uint32_t)(p.K % BK);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t c16 = 16u * lch[e];
+        L.vw[e] = L.wgroups ? (uint32_t)((wrow0 + lrow) * p.ldw) + c16 : OOB;
+        L.va[e] = L.agroups ? (uint32_t)((arow0 + lrow) * p.lda) + c16 : OOB;
+        const bool cut = ktail != 0 && c16 >= ktail;
+        L.vw_t[e] = cut ? OOB : L.vw[e];
+        L.va_t[e] = cut ? OOB : L.va[e];
+    }
+    L.row8_w = (uint32_t)(8 * p.ldw);
+    L.row8_a = (uint32_t)(8 * p.lda);
+    L.rsa = buffer_desc(p.sa, p.sa_stride ? (uint32_t)((p.M - 1) * p.sa_stride * 4 + 4) : 4u);
+    L.rsb = buffer_desc(p.sb, p.sb_stride ? (uint32_t)((p.w_rows - 1) * p.sb_stride * 4 + 4) : 4u);
+    const uint32_t set = lds0 + W192_SCALES_OFF;
+    L.dsa = wave < 2 ? set + 256u * (uint32_t)wave : lds0 + W192_JUNK_OFF;
+    L.dsb = wave < 3 ? set + 1024u + 256u * (uint32_t)wave : lds0 + W192_JUNK_OFF;
+    const int64_t srow = (int64_t)tm * W192_TR + 64 * wave + lane;
+    L.sa_off = (wave < 2 && srow < p.M) ? (uint32_t)(srow * p.sa_stride * 4) : OOB;
+    const int64_t wr = (int64_t)tn * W192_WR + 64 * wave + lane;
+    L.sb_off = (wave < 3 && wr < p.N) ? (uint32_t)(wr * p.sb_stride * 4) : OOB;
+}
+
+// Load j (0..11) of k-step kl into stage `st`: 0..5 the wave's weight rows (8 per instruction), 6..9 its token rows,
+// 10 / 11 the scales (into the scale set at k-step 0, else into the scratch slot).  K-steps past the last one load
+// zeros (every k-step issues the same 12 loads, which the vmcnt waits count on).
+__device__ __forceinline__ void w192_issue_one(const W192Loader& L, int kl, uint32_t st, uint32_t lds0, int wave,
+                                               int j) {
+    const bool live = kl < L.nk;
+    const bool last = kl == L.nk - 1;
+    const uint32_t k0 = (uint32_t)kl * BK;
+    if (j < 6) {
+        const uint32_t off = last ? L.vw_t[j & 1] : L.vw[j & 1];
+        const bool ok = live && j < L.wgroups && off != OOB;
+        dma16(L.rw, st + (uint32_t)(48 * wave + 8 * j) * ROWB, ok ? off + k0 + (uint32_t)j * L.row8_w : OOB);
+    } else if (j < 10) {
+        const int i = j - 6;
+        const uint32_t off = last ? L.va_t[i & 1] : L.va[i & 1];
+        const bool ok = live && i < L.agroups && off != OOB;
+        dma16(L.ra, st + W192_A + (uint32_t)(32 * wave + 8 * i) * ROWB, ok ? off + k0 + (uint32_t)i * L.row8_a : OOB);
+    } else {
+        const bool real = kl == 0;
+        if (j == 10) dma4(L.rsa, real ? L.dsa : lds0 + W192_JUNK_OFF, real ? L.sa_off : OOB);
+        else dma4(L.rsb, real ? L.dsb : lds0 + W192_JUNK_OFF, real ? L.sb_off : OOB);
+    }
+}
+
+// Fragment f of a sub-step (0..2: the wave's three 32-row weight blocks; 3, 4: its two 32-row token blocks).
+__device__ __forceinline__ void w192_read(const uint8_t* stage, int wn, int wm, int lane, int sub, int f, v8i af[3],
+                                          v8i bf[2]) {
+    if (f < 3) af[f] = read_frag(stage + (wn * 96 + 32 * f) * ROWB, lane, sub);
+    else bf[f - 3] = read_frag(stage + W192_A + (wm * 64 + 32 * (f - 3)) * ROWB, lane, sub);
+}
+
+__device__ __forceinline__ void w192_mfma(v16f acc[3][2], const v8i af[3], const v8i bf[2], int t) {
+    acc[t >> 1][t & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[t >> 1], bf[t & 1], acc[t >> 1][t & 1], 0, 0,
+                                                                         0, 0, 0, 0);
+}
+
+// K-step ks over 12 MFMA slots (u < 6 sub-step 0, u >= 6 sub-step 1):
+//   u < 5        the 5 sub-step-1 fragment reads of stage ks;
+//   u == 5       lgkmcnt(0) + vmcnt(12) + barrier: every wave's reads of stage ks have returned (it is free) and k-step
+//                ks + 1 has landed (only the loads of k-step ks + 2 may still be in flight);
+//   6 <= u < 12  the 12 loads of k-step ks + 3 into stage ks, two per MFMA;
+//   6 <= u < 11  the 5 sub-step-0 fragment reads of k-step ks + 1.
+template <bool READ_NEXT>
+__device__ __forceinline__ void w192_kstep(uint8_t* lds, uint32_t lds0, int s0, int ks, const W192Loader& L, int wave,
+                                           int wn, int wm, int lane, v16f acc[3][2], v8i fa0[3], v8i fb0[2],
+                                           v8i fa1[3], v8i fb1[2]) {
+    const int s1 = s0 == W192_NSTAGE - 1 ? 0 : s0 + 1;
+    const uint8_t* cur = lds + s0 * W192_STAGE;
+    const uint8_t* nxt = lds + s1 * W192_STAGE;
+    const uint32_t st = lds0 + (uint32_t)s0 * W192_STAGE;
+    constexpr int NEXT_ORDER[5] = {0, 3, 4, 1, 2};      // weight block 0 and the token blocks first: MFMA t uses
+                                                        // weight block t / 2 and token block t % 2
+#pragma unroll
+    for (int u = 0; u < 12; ++u) {
+        if (u < 6) w192_mfma(acc, fa0, fb0, u);
+        else w192_mfma(acc, fa1, fb1, u - 6);
+        if (u < 5) w192_read(cur, wn, wm, lane, 1, u, fa1, fb1);
+        if (u == 5) {
+            wait_lgkm0();
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(W192_LOADS));
+            barrier_nofence();
+        }
+        if (u >= 6) {
+            w192_issue_one(L, ks + 3, st, lds0, wave, 2 * (u - 6));
+            w192_issue_one(L, ks + 3, st, lds0, wave, 2 * (u - 6) + 1);
+        }
+        if (READ_NEXT && u >= 6 && u < 11) w192_read(nxt, wn, wm, lane, 0, NEXT_ORDER[u - 6], fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// One tile per workgroup: the launch has exactly as many workgroups as tiles, all resident at once (at most one per
+// CU), so there is no persistent loop.
+template <int OUT_DT, bool HAS_BIAS, int EPI>
+__global__ void __launch_bounds__(256, 1) gemm_w192_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[W192_LDS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wn = wave & 1, wm = wave >> 1;
+    const uint32_t lds0 = lds_addr(lds);
+    const int tiles_m = (p.M + W192_TR - 1) / W192_TR, tiles_n = (p.N + W192_WR - 1) / W192_WR;
+    int tm, tn;
+    tile_of((int)blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, p.group_m, tm, tn);
+    W192Loader L;
+    w192_loader_set(L, p, tm, tn, lds0, wave, lane);
+    // prologue: k-steps 0, 1, 2 in flight (12 loads each), then stage 0 published
+#pragma unroll
+    for (int s = 0; s < W192_NSTAGE; ++s) {
+#pragma unroll
+        for (int j = 0; j < W192_LOADS; ++j) w192_issue_one(L, s, lds0 + (uint32_t)s * W192_STAGE, lds0, wave, j);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * W192_LOADS));
+    barrier_nofence();
+    v8i fa0[3], fb0[2], fa1[3], fb1[2];
+#pragma unroll
+    for (int f = 0; f < 5; ++f) w192_read(lds, wn, wm, lane, 0, f, fa0, fb0);
+    v16f acc[3][2];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    int s0 = 0;
+    for (int ks = 0; ks < L.nk - 1; ++ks) {
+        w192_kstep<true>(lds, lds0, s0, ks, L, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        s0 = s0 == W192_NSTAGE - 1 ? 0 : s0 + 1;
+    }
+    w192_kstep<false>(lds, lds0, s0, L.nk - 1, L, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+    const float* sa_l = reinterpret_cast<const float*>(lds + W192_SCALES_OFF);
+    reg_epilogue<OUT_DT, HAS_BIAS, EPI, 3, 2>(p, tn * W192_WR + wn * 96, tm * W192_TR + wm * 64, sa_l, wm * 64,
+                                              sa_l + 256, wn * 96, lane, acc);
+    wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
+}
+
 __global__ void __launch_bounds__(256) fill_zero_kernel(float* p, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -1356,11 +1543,31 @@ int dispatch_half3(const GroupedParams& gp, int epi, int out_dt, bool has_bias, 
     return has_bias ? launch_half3<1, true, EPI_PLAIN>(gp, st) : launch_half3<1, false, EPI_PLAIN>(gp, st);
 }
 
+template <int OUT_DT, bool HAS_BIAS, int EPI>
+int launch_w192(const GemmParams& p, int tiles, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_w192_kernel<OUT_DT, HAS_BIAS, EPI>), dim3(tiles), dim3(256), 0, st, p);
+    H3_CHECK_HIP(hipGetLastError());
+    return H3FP8_OK;
+}
+
+int dispatch_w192(const GemmParams& p, int tiles, int epi, int out_dt, bool has_bias, hipStream_t st) {
+    if (out_dt == H3FP8_DT_F32) return launch_w192<H3FP8_DT_F32, false, EPI_PLAIN>(p, tiles, st);
+    if (epi == EPI_AMAX) {
+        if (out_dt == H3FP8_DT_BF16)
+            return has_bias ? launch_w192<0, true, EPI_AMAX>(p, tiles, st) : launch_w192<0, false, EPI_AMAX>(p, tiles, st);
+        return has_bias ? launch_w192<1, true, EPI_AMAX>(p, tiles, st) : launch_w192<1, false, EPI_AMAX>(p, tiles, st);
+    }
+    if (out_dt == H3FP8_DT_BF16)
+        return has_bias ? launch_w192<0, true, EPI_PLAIN>(p, tiles, st) : launch_w192<0, false, EPI_PLAIN>(p, tiles, st);
+    return has_bias ? launch_w192<1, true, EPI_PLAIN>(p, tiles, st) : launch_w192<1, false, EPI_PLAIN>(p, tiles, st);
+}
+
 // The last, partial round of a launch with full tiles leaves most CUs idle.  When its tiles fit one round as half
 // tiles (256 tokens x 128 channels, the same MFMAs per output element, so the same bits), the full-tile launch stops
 // at the last whole round and a half-tile launch covers the rest: a problem of T full tiles on G CUs runs
 // floor(T / G) full rounds and, if T mod G <= G / 2, the remainder as 2 (T mod G) half tiles.  Kernel 3 (SwiGLU pairs
-// gate and up rows inside a tile) always runs full tiles.
+// gate and up rows inside a tile) always runs full tiles.  A problem that runs as half tiles alone takes 128 x 192
+// tiles instead when they occupy more CUs and still fit one round (gemm_w192_kernel).
 int launch_split(GroupedParams gp, int epi, int out_dt, bool has_bias, hipStream_t st) {
     const int T = gp.g[0].tiles_m * gp.g[0].tiles_n;
     const int G = h3host::cu_count();
@@ -1368,6 +1575,11 @@ int launch_split(GroupedParams gp, int epi, int out_dt, bool has_bias, hipStream
     const int rest = T - full;
     const bool half = rest > 0 && 2 * rest <= G;
     const int full_tiles = half ? full : T;
+    if (full_tiles == 0) {
+        const GemmParams& p = gp.g[0];
+        const int64_t w192 = (int64_t)((p.M + W192_TR - 1) / W192_TR) * ((p.N + W192_WR - 1) / W192_WR);
+        if (w192 <= G && w192 > 2 * (int64_t)rest) return dispatch_w192(p, (int)w192, epi, out_dt, has_bias, st);
+    }
     int rc = H3FP8_OK;
     if (full_tiles > 0) {
         gp.total_tiles = full_tiles;

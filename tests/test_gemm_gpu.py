@@ -56,8 +56,11 @@ def test_integer_inputs_exact_with_guards(cuda, M, N, K):
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("scalar", ["none", "sa", "sb"])
-def test_integer_inputs_dtypes_bias_scalars(cuda, out_dtype, bias, scalar):
-    M, N, K = 300, 528, 768
+@pytest.mark.parametrize("N", [528, 400])
+def test_integer_inputs_dtypes_bias_scalars(cuda, out_dtype, bias, scalar, N):
+    """Output dtypes, bias and scalar scales, exact on integer operands; N = 528 runs as 12 half tiles, N = 400 as
+    9 tiles of 128 x 192 (ragged in both M and N)."""
+    M, K = 300, 768
     a, w, sa, sb = int_operands(M, N, K, seed=11, device=cuda)
     if scalar == "sa":
         sa = sa[:1].reshape(())
@@ -94,7 +97,8 @@ def test_measured_shapes_within_tolerance(cuda, name):
 @pytest.mark.parametrize("M,N,K", [(777, 3072, 1024), (4100, 4368, 256), (2300, 3600, 256)])
 def test_fused_row_amax_and_quant(cuda, M, N, K):
     """The fused next-layer quant: the row maxima and the quant from them equal the plain GEMM's output and kernel 1 on
-    it, for half tiles only (48 tiles), whole rounds plus a half-tile tail (306) and full tiles only (135)."""
+    it, for 128 x 192 tiles (48 full tiles run as 112 of these), whole rounds plus a half-tile tail (306) and full tiles
+    only (135)."""
     from h3_tp2_amd import ops
     a, w, sa, sb = serving_like(M, N, K, seed=3 + M, device=cuda)
     amax = torch.full((M,), 123.0, device=cuda)          # the library zeroes it first
@@ -204,9 +208,10 @@ def test_accumulator_error_model(cuda, kind, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(16740, 9216, 3072), (2048, 3072, 3072), (31248, 3072, 1024)])
 def test_half_tile_tail_equals_full_tiles(cuda, M, N, K):
-    """A launch whose last round runs as half tiles (256 x 128) gives the same bits as all full tiles (the grouped
-    path never splits): the same MFMA sequence per output element.  Also the fused row maxima + quant through the
-    split launch against the oracle's quant of its own output."""
+    """A launch whose last round runs as half tiles (256 x 128), or whose whole problem runs as 128 x 192 tiles (2048 x
+    3072: 256 of them), gives the same bits as all full tiles (the grouped path never splits): the same MFMA sequence
+    per output element.  Also the fused row maxima + quant through the split launch against the oracle's quant of its
+    own output."""
     from h3_tp2_amd import ops
     a, w, sa, sb = serving_like(M, N, K, seed=7, device=cuda)
     y = _gemm(a, w, sa, sb)
@@ -220,11 +225,12 @@ def test_half_tile_tail_equals_full_tiles(cuda, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4352, 128), (4100, 4368, 64), (5000, 2560, 64), (2300, 3600, 192),
-                                   (1000, 3008, 96), (6000, 2816, 48)])
+                                   (1000, 3008, 96), (6000, 2816, 48), (2048, 4096, 64), (300, 400, 176)])
 def test_integer_inputs_exact_launch_splits(cuda, M, N, K):
     """Shapes whose tile counts take each launch form on 256 CUs: whole rounds plus a half-tile tail (272, 306 and 264
-    tiles), full tiles only (200 and 135 tiles), half tiles only (48 tiles); K below one 128-deep k-step; integer
-    operands, so the output must equal the oracle bit for bit, with guard sentinels around it."""
+    tiles), full tiles only (200 and 135 tiles), half tiles only (128 tiles), 128 x 192 tiles (48 full tiles as 128
+    of these; 4 as 9, ragged in M, N and K); K below one 128-deep k-step; integer operands, so the output must equal
+    the oracle bit for bit, with guard sentinels around it."""
     from h3_tp2_amd import ops
     a, w, sa, sb = int_operands(M, N, K, seed=7 * M + N + K, device=cuda)
     ref = ref_gemm(a, w, sa, sb)
