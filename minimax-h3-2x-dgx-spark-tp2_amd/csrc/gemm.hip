@@ -39,7 +39,8 @@
 // instead.  Both give the same table entry, so the output does not depend on the path taken.
 // Other forms below, each with the same MFMA sequence per output element (so the same bits): the half-tile kernel
 // (256 tokens x 128 channels, three stages) for a problem's last partial round and for problems of fewer tiles than
-// CUs, and the small-M form (M <= 32: one wave per 16 weight rows, the weight streamed once).
+// CUs, the 128 x 192 tiles (one per CU) for such problems when they occupy more CUs than the half tiles would, and
+// the small-M form (M <= 32: one wave per 16 weight rows, the weight streamed once).
 #include <algorithm>
 
 #include "h3fp8_common.h"
