@@ -331,16 +331,27 @@ __device__ __forceinline__ void make_loader(const GemmParams& p, int tm, int tn,
 // a k-step's loads need is prepared per tile here, so that the k-step itself adds only k0 to four offsets.
 struct Cursor {
     Loader L;
-    int c;          // workgroup-local tile ordinal (global tile id = blockIdx.x + c * gridDim.x)
+    int c;          // workgroup-local tile ordinal (global tile id: round_id(blockIdx.x, c, gridDim.x))
     int ks, nk;
     bool valid;
     uint32_t dsa, dsb;  // LDS addresses of this wave's share of the tile's scale set (set c % NSCALE)
 };
 
+// Tile id of workgroup b in its round c of a persistent launch over G workgroups: b + c G; a grouped launch takes the
+// workgroups of each XCD (b & 7) in reverse order on odd rounds (a bijection of the round onto itself that keeps every
+// id on its XCD), so that the workgroups that drew the longest tiles of one round draw the shortest of the next.  The
+// groups' tiles are laid out by descending K, and a round-robin that always starts at workgroup 0 leaves the first
+// workgroups with the most k-steps (the four-group workload: 271 against a mean of 252; serpentine 259).
+template <bool GROUPED>
+__device__ __forceinline__ int round_id(int b, int c, int G) {
+    if (!GROUPED || !(c & 1) || (G & 7)) return b + c * G;
+    return c * G + ((((G >> 3) - 1 - (b >> 3)) << 3) | (b & 7));
+}
+
 template <int EPI, bool GROUPED>
 __device__ __forceinline__ void cursor_set(Cursor& I, const GroupedParams& gp, int c, uint32_t lds0, int wave,
                                            int lane) {
-    const int id = (int)blockIdx.x + c * (int)gridDim.x;
+    const int id = round_id<GROUPED>((int)blockIdx.x, c, (int)gridDim.x);
     I.c = c;
     I.ks = 0;
     I.valid = id < gp.total_tiles;
@@ -807,7 +818,7 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
 
     int g = 0;
     for (int c = 0;; ++c) {
-        const int id = (int)blockIdx.x + c * G;
+        const int id = round_id<GROUPED>((int)blockIdx.x, c, G);
         int tm, tn;
         const int pi = locate<GROUPED>(gp, id, tm, tn);
         const GemmParams& p = gp.g[pi];
@@ -833,7 +844,7 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
         epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
         // the next tile's fragment reads stay after the epilogue: hoisted into it they would hold 64 VGPRs across it
         __builtin_amdgcn_sched_barrier(0);
-        if (id + G >= gp.total_tiles) break;
+        if ((GROUPED ? round_id<GROUPED>((int)blockIdx.x, c + 1, G) : id + G) >= gp.total_tiles) break;
         read_frags<EPI>(lds + (g & 1) * STAGE_BYTES, wn, wm, lane, 0, fa0, fb0);
     }
     wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
