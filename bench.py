@@ -13,8 +13,9 @@ timed steps is bracketed by HIP events on the launch stream, so the per-kernel a
 against the 5.0 PFLOP/s FP8 dense MFMA peak.  Before the warm-up steps an explicit pre-roll runs the chain for
 ``--preroll-s`` seconds: the chip's clock moves over the first heavy calls, and the pre-roll makes the timed steps
 independent of how short the warm-up is.  The other measured workloads (the QKV projection at 960x576, the single
-linear, the FFN at 1344x768 5 s, the grouped launch, the producers / consumers passes, the vendor GEMM) are reported
-under ``workloads``.  ``cpu_baseline`` times the reference's torch CPU path (oracle/torch_path.py) of the same chain on
+linear, the FFN at 1344x768 5 s, the grouped launch, the reference's four H3 linears at its per-rank M = 42 848, the
+host cost of one dispatched call, the producers / consumers passes, the vendor GEMM) are reported under
+``workloads``.  ``cpu_baseline`` times the reference's torch CPU path (oracle/torch_path.py) of the same chain on
 a row sample, on this host's cores.  Synthetic seeded inputs, random-init weights (no checkpoints).
 """
 from __future__ import annotations
@@ -390,6 +391,111 @@ def main() -> None:
             "form": f"kernel 2's small-M form on [{Mg},{Kg}] x [{Ng},{Kg}]: {Ng // 16} waves of 16 weight rows, "
                     "the weight streamed once (output bitwise the tiled kernel's)"}
         del probs, xs
+
+    if want("h3_linears"):
+        # The reference's own H3 DiT linears at its published per-rank row count M = 42 848 (qkv 5376 -> 21 504, out
+        # 7168 -> 5376, fc1 5376 -> 2 x 14 336 with the SwiGLU epilogue and the requant tail, fc2 14 336 -> 5376),
+        # log-normal activation rows exp(N(0, 1) 1.5) (its probe inputs), each launch timed by events inside the timed
+        # steps.
+        Mh = 42848
+        specs = [("qkv 5376->21504 (kernel 2)", 5376, 21504, False), ("out 7168->5376 (kernel 2)", 7168, 5376, False),
+                 ("fc1 5376->2x14336 + SwiGLU + row amax (kernel 3)", 5376, 28672, True),
+                 ("fc2 14336->5376 (kernel 2)", 14336, 5376, False)]
+        launches = []
+        genh = torch.Generator(device=dev).manual_seed(40)
+        for i, (name, Kh, Nh, swiglu) in enumerate(specs):
+            # made on the device (a timing workload; 0.6 G elements would take the host ~10 s)
+            xh = (torch.randn(Mh, Kh, device=dev, generator=genh)
+                  * torch.exp(torch.randn(Mh, 1, device=dev, generator=genh) * 1.5)).to(torch.bfloat16)
+            ah, sah = ops.quant_rows(xh)
+            del xh
+            wh, swh = quantised_weight(Nh, Kh, seed=50 + i)
+            if swiglu:
+                hh, amh = buf((Mh, Nh // 2), torch.bfloat16), buf((Mh,), torch.float32)
+                qhh, shh = buf((Mh, Nh // 2), E4), buf((Mh, 1), torch.float32)
+                launches.append((name, (lambda a_=ah, w_=wh, s_=sah, t_=swh, h_=hh, m_=amh:
+                                        ops.gemm_swiglu(a_, w_, s_, t_, row_amax=m_, out=h_)), 2.0 * Mh * Nh * Kh, 0.0))
+                launches.append(("fc1 requant tail [M,14336]", (lambda h_=hh, m_=amh, q_=qhh, s_=shh:
+                                                                ops.quant_rows_amax(h_, m_, q_, s_)),
+                                 0.0, 3.0 * Mh * (Nh // 2) + 4.0 * Mh))
+            else:
+                yh = buf((Mh, Nh), torch.bfloat16)
+                launches.append((name, (lambda a_=ah, w_=wh, s_=sah, t_=swh, y_=yh:
+                                        ops.gemm(a_, w_, s_, t_, torch.bfloat16, out=y_)), 2.0 * Mh * Nh * Kh, 0.0))
+        hsteps = max(5, steps // 3)
+        for _ in range(3):
+            for _, fn, _, _ in launches:
+                fn()
+        hm = [[ev() for _ in range(len(launches) + 1)] for _ in range(hsteps)]
+        torch.cuda.synchronize()
+        for k in range(hsteps):
+            for i, (_, fn, _, _) in enumerate(launches):
+                hm[k][i].record(stream)
+                fn()
+            hm[k][-1].record(stream)
+        hm[-1][-1].synchronize()
+        lm = [sum(hm[k][i].elapsed_time(hm[k][i + 1]) for k in range(hsteps)) / hsteps for i in range(len(launches))]
+        hres = {}
+        for (name, _, f, b), ms in zip(launches, lm):
+            hres[name] = ({"ms": round(ms, 4), "TFLOP/s": round(tflops(f, ms), 1),
+                           "frac_mfma": round(tflops(f, ms) / PEAK_TFLOPS, 4)} if f else
+                          {"ms": round(ms, 4), "GB/s": round(gbs(b, ms), 1), "frac_hbm": round(gbs(b, ms) / PEAK_GBS, 4)})
+        fh = sum(f for _, _, f, _ in launches)
+        gemm_h = sum(ms for (_, _, f, _), ms in zip(launches, lm) if f)
+        out["h3_linears_42848"] = {
+            "per_launch": hres, "step_ms": round(sum(lm), 4), "TFLOP/s": round(tflops(fh, sum(lm)), 1),
+            "gemms_TFLOP/s": round(tflops(fh, gemm_h), 1), "gemms_frac_mfma": round(tflops(fh, gemm_h) / PEAK_TFLOPS, 4),
+            "note": f"the reference's H3 linear shapes at its per-rank M = {Mh}; its published GB10 figures for the same "
+                    "shapes (157-169 TFLOP/s per GEMM, another chip) are context, not a baseline"}
+        del launches
+
+    if want("dispatch"):
+        # Host cost of one eligible call through the drop-in: vLLM's ops.cutlass_scaled_mm replaced by the dispatcher
+        # (eligibility test -> route -> kernel 2's launcher -> ctypes -> the C ABI's launch), and QuantFP8.forward's
+        # replacement on a dynamic per-token instance (-> kernel 1), on a small problem whose kernels take a few us,
+        # so the host is the bound.  Wall time of 2000 back-to-back calls / 2000, with torch._scaled_mm (hipBLASLt) on
+        # the same call for scale (the reference measures its dispatcher the same way against it).
+        import types
+        from h3_tp2_amd import fp8_gemm, fp8_quant_fuse
+        Md, Nd, Kd = 32, 1024, 1024
+        xd = synthetic.activations(Md, Kd, seed=60, n_out=1).to(dev)
+        ad, sad = ops.quant_rows(xd)
+        wd_, swd = quantised_weight(Nd, Kd, seed=61)
+        bd = wd_.t()
+        shim = types.SimpleNamespace(cutlass_scaled_mm=lambda *a, **k: None)
+        saved_state = dict(fp8_gemm._state)
+        fp8_gemm.install(shim, level="hip", check=False)
+        qf = types.SimpleNamespace(static=False, use_per_token_if_dynamic=True, is_group_quant=False,
+                                   num_token_padding=None)
+        saved_k1 = fp8_quant_fuse._state.get("kernel1")
+        fp8_quant_fuse._state["kernel1"] = True
+        qfwd = fp8_quant_fuse.make_quant_forward(lambda self, x, *a, **k: None)
+
+        def host_us(fn, n=2000):
+            for _ in range(100):
+                fn()
+            torch.cuda.synchronize()
+            t_a = time.perf_counter()
+            for _ in range(n):
+                fn()
+            t_b = time.perf_counter()
+            torch.cuda.synchronize()
+            return (t_b - t_a) / n * 1e6
+        sa2d, sb2d = sad.view(Md, 1), swd.view(1, Nd)
+        res_d = {
+            "shape": f"M={Md} N={Nd} K={Kd}",
+            "dispatcher_cutlass_scaled_mm_us": round(host_us(lambda: shim.cutlass_scaled_mm(ad, bd, sad, swd,
+                                                                                            torch.bfloat16)), 2),
+            "ops_gemm_us": round(host_us(lambda: ops.gemm(ad, wd_, sad, swd)), 2),
+            "torch_scaled_mm_us": round(host_us(lambda: torch._scaled_mm(ad, bd, sa2d, sb2d,
+                                                                         out_dtype=torch.bfloat16)), 2),
+            "quantfp8_forward_us": round(host_us(lambda: qfwd(qf, xd)), 2),
+            "ops_quant_rows_us": round(host_us(lambda: ops.quant_rows(xd)), 2),
+            "calls": 2000}
+        out["dispatch_host_cost"] = res_d
+        fp8_gemm._state.clear()
+        fp8_gemm._state.update(saved_state)
+        fp8_quant_fuse._state["kernel1"] = saved_k1
 
     if want("producers"):
         # The quant fused into its producers: norm1 + AdaLN -> QKV input at the 960x576 5 s token count, the gated

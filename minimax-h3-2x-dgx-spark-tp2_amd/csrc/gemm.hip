@@ -902,7 +902,8 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
         arow[i] = m < p.M ? (uint32_t)((int64_t)m * p.lda) : OOB;
     }
     const int nk = (p.K + BK - 1) / BK;
-    // the 4 + MB loads of k-step ks into ring slot `slot`: pieces at or past K read zeros (K % 16 == 0)
+    // the RowsRing<MB>::LOADS = ROWS_RW / 8 + MB loads of k-step ks into ring slot `slot`: pieces at or past K read
+    // zeros (K % 16 == 0)
     auto issue = [&](int slot, int ks) {
         const uint32_t st = lds0 + (uint32_t)slot * ROWS_STAGE;
 #pragma unroll
@@ -933,8 +934,8 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
 #pragma unroll
     for (int s = 0; s < ROWS_DEPTH; ++s) issue(s, s);
-    // every k-step issues 4 + MB loads (past the last k-step out of range, touching no memory), so when k-step ks is
-    // consumed exactly the loads of the ROWS_DEPTH - 1 younger k-steps may still be in flight
+    // every k-step issues ROWS_RW / 8 + MB loads (RowsRing::LOADS; past the last k-step out of range, touching no
+    // memory), so when k-step ks is consumed exactly the loads of the ROWS_DEPTH - 1 younger k-steps may be in flight
     int ks = 0;
     for (; ks + ROWS_DEPTH <= nk; ks += ROWS_DEPTH) {
 #pragma unroll
@@ -1588,7 +1589,10 @@ int launch_split(GroupedParams gp, int epi, int out_dt, bool has_bias, hipStream
     const int G = h3host::cu_count();
     const int full = (epi == EPI_SWIGLU) ? T : (T / G) * G;
     const int rest = T - full;
-    const bool half = rest > 0 && 2 * rest <= G;
+    // half_tile_of takes the full-tile launch to have covered the first full / 8 positions of each per-XCD range,
+    // which holds when full is a multiple of 8 (a CU count that is a multiple of 8, as on gfx950); otherwise the
+    // launch keeps full tiles throughout
+    const bool half = rest > 0 && 2 * rest <= G && full % 8 == 0;
     const int full_tiles = half ? full : T;
     if (full_tiles == 0) {
         const GemmParams& p = gp.g[0];
@@ -1693,6 +1697,7 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
 namespace h3host {
 int quant_rows_amax_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row_amax, void* q,
                            int64_t ldq, float* scale, hipStream_t st);
+int quant_args_ok(const void* x, int64_t ldx, int64_t M, int64_t K, const void* q, int64_t ldq, const float* scale);
 }
 
 // ---- the library-owned row-maxima buffer of h3fp8_gemm_quant_noalloc -------------------------------------------------
@@ -1747,7 +1752,10 @@ int h3fp8_gemm_quant(const void* a, int64_t lda, const void* w, int64_t ldw, con
                      const float* sb, int64_t sb_stride, const void* bias, void* y, int64_t ldy, int64_t M, int64_t N,
                      int64_t K, float* amax_ws, void* q, int64_t ldq, float* scale, void* stream) {
     H3_REQUIRE(M == 0 || (amax_ws && q && scale), "h3fp8_gemm_quant: null workspace or output");
-    int rc = h3fp8_gemm(a, lda, w, ldw, sa, sa_stride, sb, sb_stride, bias, y, ldy, H3FP8_DT_BF16, M, N, K, amax_ws,
+    // the tail's arguments are checked before the GEMM is enqueued: a bad ldq leaves nothing launched
+    int rc = h3host::quant_args_ok(y, ldy, M, N, q, ldq, scale);
+    if (rc) return rc;
+    rc = h3fp8_gemm(a, lda, w, ldw, sa, sa_stride, sb, sb_stride, bias, y, ldy, H3FP8_DT_BF16, M, N, K, amax_ws,
                         stream);
     if (rc) return rc;
     return h3host::quant_rows_amax_launch(y, ldy, M, N, amax_ws, q, ldq, scale, (hipStream_t)stream);
@@ -1762,6 +1770,9 @@ int h3fp8_gemm_quant_noalloc(const void* a, int64_t lda, const void* w, int64_t 
                "workspace)", (long long)M, H3FP8_NOALLOC_MAX_ROWS);
     H3_REQUIRE(M == 0 || (q && scale), "h3fp8_gemm_quant_noalloc: null output");
     int rc = check_gemm(a, lda, w, ldw, sa, sa_stride, sb, sb_stride, y, ldy, M, N, K, N, "h3fp8_gemm_quant_noalloc");
+    if (rc) return rc;
+    // the tail's arguments too, before the fill and the GEMM are enqueued (nothing is launched for a refused call)
+    rc = h3host::quant_args_ok(y, ldy, M, N, q, ldq, scale);
     if (rc) return rc;
     if (M == 0 || N == 0) return H3FP8_OK;
     // no set-up here (it creates a stream and waits): the caller has run h3fp8_init on this device
@@ -1802,7 +1813,9 @@ int h3fp8_gemm_swiglu_quant(const void* a, int64_t lda, const void* w_gate_up, i
                             int64_t F, int64_t K, void* h_ws, float* amax_ws, void* q, int64_t ldq, float* scale,
                             void* stream) {
     H3_REQUIRE(M == 0 || (h_ws && amax_ws && q && scale), "h3fp8_gemm_swiglu_quant: null workspace or output");
-    int rc = h3fp8_gemm_swiglu(a, lda, w_gate_up, ldw, sa, sa_stride, sb, sb_stride, bias, h_ws, F, amax_ws, M, F, K,
+    int rc = h3host::quant_args_ok(h_ws, F, M, F, q, ldq, scale);
+    if (rc) return rc;
+    rc = h3fp8_gemm_swiglu(a, lda, w_gate_up, ldw, sa, sa_stride, sb, sb_stride, bias, h_ws, F, amax_ws, M, F, K,
                                stream);
     if (rc) return rc;
     return h3host::quant_rows_amax_launch(h_ws, F, M, F, amax_ws, q, ldq, scale, (hipStream_t)stream);

@@ -254,6 +254,11 @@ __global__ void __launch_bounds__(256) quant_segments_kernel(const uint16_t* __r
 
 namespace h3host {
 // Used by the fused GEMM paths for their tail pass.
+// The quant tail's argument checks alone, for entry points that must refuse a bad call before their first launch.
+int quant_args_ok(const void* x, int64_t ldx, int64_t M, int64_t K, const void* q, int64_t ldq, const float* scale) {
+    return check_quant_args(x, ldx, M, K, q, ldq, scale);
+}
+
 int quant_rows_amax_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row_amax, void* q,
                            int64_t ldq, float* scale, hipStream_t st) {
     int rc = check_quant_args(x, ldx, M, K, q, ldq, scale);

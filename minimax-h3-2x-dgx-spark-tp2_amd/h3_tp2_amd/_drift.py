@@ -9,6 +9,14 @@ value (``REVIEWED``): the sha256 (first 16 hex digits) of the function's source 
 space, with empty lines, comment lines and decorator lines dropped.  A changed, missing or foreign-wrapped function
 leaves the site stock, with a warning naming it.
 
+The four functions the transformer module calls by name (``fused_qk_norm_rope``, ``indexed_gate``,
+``indexed_gate_rms_norm_scale_shift``, ``rms_norm_indexed_scale_shift``) are fingerprinted in their upstream module,
+and the transformer's binding must be that very function (h3_tp2/fp8_consumers.py:849-855, fp8_quant_fuse.py:891-892):
+a wrapper installed there by someone else -- with ``functools.wraps`` or without -- is drift, since a fused site would
+replace the call and drop what the wrapper does.  Only this library's own wrappers are seen through: functions whose
+code lives in this package (``functools.wraps`` copies names and attributes, never the code object) that carry an
+``_h3_tp2_amd*`` marker and say what they wrap in ``__wrapped__``.
+
 ``REVIEWED`` holds the fingerprints of vLLM-Omni v0.30.0 (commit a8576ccb7) and vLLM 0.30.0 -- the upstream the
 reference's sites were reviewed against (h3_tp2/fp8_consumers.py:64-80, h3_tp2/fp8_quant_fuse.py:857-877); they are
 facts about those sources under this normalisation, so they carry over unchanged.
@@ -17,7 +25,11 @@ from __future__ import annotations
 
 import hashlib
 import inspect
+import os
 from typing import Any, Callable
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+WRAPPED = "wrapped"      # a by-name binding that is not the upstream function (nor this library's wrapper of it)
 
 REVIEWED = {
     # vllm_omni/diffusion/models/minimax_h3/minimax_h3_transformer.py
@@ -80,14 +92,44 @@ def fingerprint_source(src: str) -> str:
     return hashlib.sha256("\n".join(normalised_lines(src)).encode()).hexdigest()[:16]
 
 
+def is_own_wrapper(fn: Any) -> bool:
+    """True for a wrapper this library installed: its code is defined in this package, it carries an ``_h3_tp2_amd*``
+    marker and names what it wraps in ``__wrapped__``."""
+    code = getattr(fn, "__code__", None)
+    if code is None or getattr(fn, "__wrapped__", None) is None:
+        return False
+    if os.path.dirname(os.path.abspath(code.co_filename)) != _PKG_DIR:
+        return False
+    return any(k.startswith("_h3_tp2_amd") for k in vars(fn))
+
+
+def own_unwrap(fn: Any) -> Any:
+    """``fn`` with this library's own wrappers taken off (any other wrapper stays)."""
+    for _ in range(16):
+        if not is_own_wrapper(fn):
+            break
+        fn = fn.__wrapped__
+    return fn
+
+
 def fingerprint(fn: Any) -> str | None:
-    """The fingerprint of a function's source (a Triton kernel's ``fn``; functools.wraps wrappers are seen through);
-    None when its source cannot be read."""
+    """The fingerprint of a function's source (a Triton kernel's ``fn``; as in the reference, ``inspect`` sees through
+    functools.wraps wrappers of methods); None when its source cannot be read."""
     fn = getattr(fn, "fn", fn)
     try:
         return fingerprint_source(inspect.getsource(fn))
     except (OSError, TypeError):
         return None
+
+
+def _bound(tr: Any, name: str, module: Any) -> Any:
+    """The upstream function ``module.name`` when the transformer module ``tr`` calls exactly it (or this library's
+    wrapper of it) under ``name``; WRAPPED when ``tr`` binds something else; None when either is absent."""
+    upstream = getattr(module, name, None) if module is not None else None
+    binding = getattr(tr, name, None)
+    if upstream is None or binding is None:
+        return None
+    return upstream if own_unwrap(binding) is upstream else WRAPPED
 
 
 def _attr(obj: Any, *path: str) -> Any:
@@ -124,15 +166,16 @@ def resolvers(tr: Any, modules: dict | None = None) -> dict[str, Callable[[], An
         "rms_norm_rope_kernel": lambda: _attr(m.get("qk"), "_rms_norm_rope_kernel"),
         "launch_fused_rms_norm_rope": lambda: _attr(m.get("qk"), "_launch_fused_rms_norm_rope"),
         "fused_qk_norm_rope_impl": lambda: _attr(m.get("qk"), "_fused_qk_norm_rope_impl"),
-        # the functions the transformer module calls by name: its own binding (a foreign wrapper there is drift)
-        "fused_qk_norm_rope": lambda: getattr(tr, "fused_qk_norm_rope", None),
+        # the functions the transformer module calls by name: the upstream module's own function, and the
+        # transformer's binding must be it (any other wrapper there is drift)
+        "fused_qk_norm_rope": lambda: _bound(tr, "fused_qk_norm_rope", m.get("qk")),
         "fused_cuda_supported": lambda: _attr(m.get("qk"), "_fused_cuda_supported"),
         "indexed_gate_kernel": lambda: _attr(m.get("im"), "_indexed_gate_kernel"),
-        "indexed_gate": lambda: getattr(tr, "indexed_gate", None),
+        "indexed_gate": lambda: _bound(tr, "indexed_gate", m.get("im")),
         "gate_rms_kernel": lambda: _attr(m.get("im"), "_indexed_gate_rms_norm_scale_shift_kernel"),
-        "gate_rms": lambda: getattr(tr, "indexed_gate_rms_norm_scale_shift", None),
+        "gate_rms": lambda: _bound(tr, "indexed_gate_rms_norm_scale_shift", m.get("im")),
         "rms_kernel": lambda: _attr(m.get("im"), "_rms_norm_indexed_scale_shift_kernel"),
-        "rms": lambda: getattr(tr, "rms_norm_indexed_scale_shift", None),
+        "rms": lambda: _bound(tr, "rms_norm_indexed_scale_shift", m.get("im")),
         "launch_row_chunks": lambda: _attr(m.get("im"), "_launch_row_chunks"),
         "silu_forward_cuda": lambda: _attr(m.get("act"), "SiluAndMul", "forward_cuda"),
         "attn_layer_forward": lambda: _attr(m.get("attn_layer"), "Attention", "forward"),
@@ -149,7 +192,7 @@ def drifted(names, found: dict[str, Callable[[], Any]], reviewed: dict[str, str]
     out = []
     for name in names:
         obj = found[name]() if name in found else None
-        got = fingerprint(obj) if obj is not None else "absent"
+        got = WRAPPED if obj is WRAPPED else fingerprint(own_unwrap(obj)) if obj is not None else "absent"
         if got != table.get(name):
             out.append(f"{name}: {got} (reviewed {table.get(name)})")
     return out

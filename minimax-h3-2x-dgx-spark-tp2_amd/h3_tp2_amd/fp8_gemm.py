@@ -56,7 +56,9 @@ def eligible(a, b, scale_a, scale_b, out_dtype, bias=None) -> bool:  # noqa: ANN
         return False
     if bias is not None and (bias.dim() != 1 or bias.numel() != N):
         return False
-    if not a.is_contiguous() or not b.t().is_contiguous() or a.shape[1] % 16 or N % 16:
+    # b.t() contiguous: the common layout is read from the strides, any other through the view
+    if not a.is_contiguous() or (b.stride() != (1, a.shape[1]) and not b.t().is_contiguous()) or a.shape[1] % 16 \
+            or N % 16:
         return False
     if a.shape[1] == 0:                                        # an empty reduction: the stock op (the kernels refuse it)
         return False
@@ -91,8 +93,9 @@ def _bias(bias, out_dtype):  # noqa: ANN001,ANN202
 
 def scaled_mm_fused(a, b, scale_a, scale_b, out_dtype, bias=None):  # noqa: ANN001,ANN201
     """Kernel 2 on an eligible call (``b`` is vLLM's [K, N] view of the [N, K] weight): one launch, the scale
-    epilogue on the accumulator (h3_tp2/fp8_gemm.py:240-248, fp8_cutlass.py:115-131)."""
-    return ops.scaled_mm(a, b, scale_a, scale_b, out_dtype, _bias(bias, out_dtype))
+    epilogue on the accumulator (h3_tp2/fp8_gemm.py:240-248, fp8_cutlass.py:115-131).  The call has passed
+    ``eligible``, so it takes the lean launcher (the C side re-checks sizes, strides and alignment)."""
+    return ops.scaled_mm_eligible(a, b, scale_a, scale_b, out_dtype, bias)
 
 
 def product_fp32(a, b) -> torch.Tensor:  # noqa: ANN001
@@ -181,24 +184,33 @@ def make_scaled_mm(orig):  # noqa: ANN001,ANN201
     return _mm
 
 
-def selfcheck(device="cuda") -> list[str]:  # noqa: ANN001
+# Install-check cases: (kind, M, N, K).  The small ones run as half tiles or 128 x 192 tiles and pin the edges; the
+# 4100-row ones are the serving shapes the reference checks at install (h3_tp2/fp8_cutlass.py:211-213) -- 17 token tiles
+# x 21 weight tiles = 357 tiles, so they run the persistent full-tile kernel on every CU and its half-tile tail.
+SELFCHECK_CASES = (("int", 200, 400, 512), ("int", 333, 272, 1024), ("int", 129, 528, 3072),
+                   ("int", 4100, 5376, 1024), ("rand", 200, 1040, 2048), ("rand", 4100, 5376, 7168),
+                   ("rand", 4100, 21504, 5376))
+
+
+def selfcheck(device="cuda", cases=SELFCHECK_CASES) -> list[str]:  # noqa: ANN001
     """Install check on the GPU (h3_tp2/fp8_cutlass.py:204-227 plays the same part): kernel 2 against the two-pass
     form and against torch's fp32 matmul of the dequantised operands on integer-valued inputs (exact accumulators in
     any order: checks the epilogue, the tile map and the edges bit for bit), with partial row and column tiles, and the
-    two forms against each other on random inputs.  Returns the failing cases."""
+    two forms against each other on random inputs, up to the 4100-row DiT serving shapes.  Operands are generated on
+    the device.  Returns the failing cases."""
     bad = []
-    g = torch.Generator(device="cpu").manual_seed(0)
-    for kind, M, N, K in (("int", 200, 400, 512), ("int", 333, 272, 1024), ("int", 129, 528, 3072),
-                          ("rand", 200, 1040, 2048)):
+    g = torch.Generator(device=device).manual_seed(0)
+    for kind, M, N, K in cases:
         if kind == "int":
-            a = torch.randint(-4, 5, (M, K), generator=g).float()
-            w = torch.randint(-2, 3, (N, K), generator=g).float()
+            a = torch.randint(-4, 5, (M, K), generator=g, device=device).float()
+            w = torch.randint(-2, 3, (N, K), generator=g, device=device).float()
         else:
-            a = (torch.randn(M, K, generator=g) * 64).clamp(-448, 448)
-            w = (torch.randn(N, K, generator=g) * 64).clamp(-448, 448)
-        sa = torch.exp(torch.empty(M, 1).uniform_(-9.0, -2.0, generator=g)).to(device)
-        sb = torch.exp(torch.empty(N).uniform_(-9.5, -7.5, generator=g)).to(device)
-        ad, wd = a.to(device).to(E4M3), w.to(device).to(E4M3)
+            a = (torch.randn(M, K, generator=g, device=device) * 64).clamp(-448, 448)
+            w = (torch.randn(N, K, generator=g, device=device) * 64).clamp(-448, 448)
+        sa = torch.exp(torch.empty(M, 1, device=device).uniform_(-9.0, -2.0, generator=g))
+        sb = torch.exp(torch.empty(N, device=device).uniform_(-9.5, -7.5, generator=g))
+        ad, wd = a.to(E4M3), w.to(E4M3)
+        del a, w
         y = scaled_mm_fused(ad, wd.t(), sa, sb, torch.bfloat16)
         y2 = scaled_mm_tensor32(ad, wd.t(), sa, sb, torch.bfloat16)
         ok = torch.equal(y.view(torch.int16), y2.view(torch.int16))
@@ -208,6 +220,7 @@ def selfcheck(device="cuda") -> list[str]:  # noqa: ANN001
             ok = ok and torch.equal(y.view(torch.int16), ref.view(torch.int16))
         if not ok:
             bad.append(f"{kind} M={M} N={N} K={K}")
+        del ad, wd, y, y2
     torch.cuda.synchronize(device)
     return bad
 

@@ -248,6 +248,7 @@ def _install_on(cls, *, level: int, lora_layer_type=()) -> bool:  # noqa: ANN001
         return self.fc2(h)[0]
 
     forward.__wrapped__ = stock_forward             # source fingerprints see the upstream forward through it
+    forward._h3_tp2_amd_swiglu = True
     cls.forward = forward
     cls._h3_tp2_amd_swiglu = True
     _state["level"] = level

@@ -22,7 +22,13 @@ MIN_SCALE = 1.0 / (FP8_MAX * 512.0)     # vLLM's minimum per-token scale (fp8_qu
 _DT = {torch.bfloat16: _lib.H3FP8_DT_BF16, torch.float16: _lib.H3FP8_DT_FP16, torch.float32: _lib.H3FP8_DT_F32}
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """The raw HIP stream of torch's current stream on ``t``'s device (the launch stream of every call)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -95,12 +101,15 @@ def quant_rows(x: torch.Tensor, q: torch.Tensor | None = None, scale: torch.Tens
     M, K = x.shape
     ldx = _rows(x, "x")
     if q is None:
-        q = torch.empty((M, K), device=x.device, dtype=E4M3)
-    check_buffer(q, "q", (M, K), E4M3, x.device)
+        q, ldq = torch.empty((M, K), device=x.device, dtype=E4M3), K
+    else:
+        check_buffer(q, "q", (M, K), E4M3, x.device)
+        ldq = _rows(q, "q")
     if scale is None:
         scale = torch.empty((M, 1), device=x.device, dtype=torch.float32)
-    _scale_out(scale, "scale", M, x.device)
-    _lib.call("h3fp8_quant_rows", x.data_ptr(), ldx, M, K, q.data_ptr(), _rows(q, "q"), scale.data_ptr(), _stream(x))
+    else:
+        _scale_out(scale, "scale", M, x.device)
+    _lib.call("h3fp8_quant_rows", x.data_ptr(), ldx, M, K, q.data_ptr(), ldq, scale.data_ptr(), _stream(x))
     return q, scale
 
 
@@ -179,13 +188,54 @@ def gemm(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch
     if bias is not None and (bias.dim() != 1 or bias.numel() != N or bias.dtype != out_dtype
                              or bias.device != a.device or not bias.is_contiguous()):
         raise ValueError("bias must be a contiguous [N] vector in the output dtype on the operands' device")
-    y = out if out is not None else torch.empty((M, N), device=a.device, dtype=out_dtype)
-    check_buffer(y, "out", (M, N), out_dtype, a.device)
+    if out is None:
+        y, ldy = torch.empty((M, N), device=a.device, dtype=out_dtype), N
+    else:
+        y = out
+        check_buffer(y, "out", (M, N), out_dtype, a.device)
+        ldy = _rows(y, "y")
     if row_amax is not None:
         check_buffer(row_amax, "row_amax", (M,), torch.float32, a.device, contiguous=True)
     _lib.call("h3fp8_gemm", a.data_ptr(), _rows(a, "a"), w.data_ptr(), _rows(w, "w"), sa.data_ptr(), sa_st,
-              sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, y.data_ptr(), _rows(y, "y"),
+              sb.data_ptr(), sb_st, bias.data_ptr() if bias is not None else None, y.data_ptr(), ldy,
               _DT[out_dtype], M, N, a.shape[1], row_amax.data_ptr() if row_amax is not None else None, _stream(a))
+    return y
+
+
+def _scale_ptr(scale: torch.Tensor) -> tuple[int, int]:
+    """(pointer, element stride) of a scale of 1 or n entries already sized by the caller's eligibility test: a scalar
+    has stride 0; [n], [n, 1] and [1, n] views are read in place; any other layout through a flattened view."""
+    if scale.numel() == 1:
+        return scale.data_ptr(), 0
+    if scale.dim() == 1 or (scale.dim() == 2 and scale.shape[1] == 1):
+        return scale.data_ptr(), scale.stride(0)
+    if scale.dim() == 2 and scale.shape[0] == 1:
+        return scale.data_ptr(), scale.stride(1)
+    flat = scale.reshape(-1)
+    return flat.data_ptr(), flat.stride(0)
+
+
+def scaled_mm_eligible(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                       out_dtype: torch.dtype, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Kernel 2 on a call that passed ``fp8_gemm.eligible`` -- the dispatcher's lean host path.  That test has checked
+    the dtypes (e4m3 operands, fp32 scales, bf16 / fp16 out), the shapes, ``a`` contiguous, ``b.t()`` contiguous, the
+    scale and bias sizes and K, N multiples of 16; what it leaves -- every operand on ``a``'s GPU, a bias in the
+    output dtype -- is checked here, and the C side checks sizes, strides and alignment again before any launch."""
+    dev = a.device
+    if not a.is_cuda:
+        raise ValueError("h3_tp2_amd kernels run on the GPU only; got a CPU tensor")
+    if scale_a.device != dev or scale_b.device != dev or (bias is not None and bias.device != dev):
+        raise ValueError("scaled_mm: every operand must be on the same GPU")
+    M, K = a.shape
+    N = b.shape[1]
+    if bias is not None and (bias.dtype != out_dtype or not bias.is_contiguous()):
+        bias = bias.to(out_dtype).contiguous()
+    sa, sa_st = _scale_ptr(scale_a)
+    sb, sb_st = _scale_ptr(scale_b)
+    y = torch.empty((M, N), device=dev, dtype=out_dtype)
+    _lib.call("h3fp8_gemm", a.data_ptr(), K, b.data_ptr(), K, sa, sa_st, sb, sb_st,
+              bias.data_ptr() if bias is not None else None, y.data_ptr(), N, _DT[out_dtype], M, N, K, None,
+              _stream(a))
     return y
 
 
@@ -268,6 +318,24 @@ def gemm_swiglu_quant(a: torch.Tensor, w_gate_up: torch.Tensor, scale_a: torch.T
     return q, s
 
 
+def _product_in(x32: torch.Tensor, name: str = "x32") -> tuple[int, int]:
+    """An fp32 product [M, W] with contiguous rows: (M, W).  The scale passes read it as fp32, so any other dtype
+    would make them read past its allocation; it is refused here, before any launch."""
+    if not isinstance(x32, torch.Tensor) or x32.dim() != 2:
+        raise ValueError(f"{name} must be a 2-D tensor")
+    if x32.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32 (the raw GEMM product), got {x32.dtype}")
+    _rows(x32, name)
+    return x32.shape[0], x32.shape[1]
+
+
+def _swiglu_width(W: int, name: str) -> int:
+    """F of a [gate | up] row of width W = 2F; the kernels take F in multiples of 4."""
+    if W % 2 or (W // 2) % 4:
+        raise ValueError(f"{name} must have an even width 2F with F a multiple of 4, got width {W}")
+    return W // 2
+
+
 def _epi_scales(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, width: int):
     M = x32.shape[0]
     s_a, sa_st = scale_vec(sa, M, "sa")
@@ -278,9 +346,10 @@ def _epi_scales(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, width: in
 def scale_swiglu(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None = None):
     """fp32 product [M, 2F] -> bf16 SwiGLU [M, F] (h3_tp2/fp8_swiglu.py:180-188)."""
     _need_cuda(x32, sa, sb)
-    M, W = x32.shape
-    F = W // 2
+    M, W = _product_in(x32)
+    F = _swiglu_width(W, "x32")
     s_a, sa_st, s_b, sb_st = _epi_scales(x32, sa, sb, W)
+    _check_bias(bias, W, x32.device)
     h = torch.empty((M, F), device=x32.device, dtype=torch.bfloat16)
     _lib.call("h3fp8_scale_swiglu", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), sa_st, s_b.data_ptr(), sb_st,
               bias.data_ptr() if bias is not None else None, M, F, h.data_ptr(), F, _stream(x32))
@@ -290,9 +359,10 @@ def scale_swiglu(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: to
 def scale_swiglu_quant(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias: torch.Tensor | None = None):
     """fp32 product [M, 2F] -> SwiGLU -> per-token quant: (q [M, F], scale [M, 1]) (h3_tp2/fp8_swiglu.py:191-200)."""
     _need_cuda(x32, sa, sb)
-    M, W = x32.shape
-    F = W // 2
+    M, W = _product_in(x32)
+    F = _swiglu_width(W, "x32")
     s_a, sa_st, s_b, sb_st = _epi_scales(x32, sa, sb, W)
+    _check_bias(bias, W, x32.device)
     q = torch.empty((M, F), device=x32.device, dtype=E4M3)
     s = torch.empty((M, 1), device=x32.device, dtype=torch.float32)
     _lib.call("h3fp8_scale_swiglu_quant", x32.data_ptr(), _rows(x32, "x32"), s_a.data_ptr(), sa_st, s_b.data_ptr(),
@@ -304,8 +374,12 @@ def scale_swiglu_quant(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bi
 def silu_mul_quant(x: torch.Tensor):
     """silu_and_mul on bf16 [M, 2F] + per-token quant: (q [M, F], scale [M, 1]) (h3_tp2/fp8_quant_fuse.py:392-402)."""
     _need_cuda(x)
+    if not isinstance(x, torch.Tensor) or x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise ValueError("silu_mul_quant takes a bf16 [M, 2F] tensor")
     M, W = x.shape
-    F = W // 2
+    F = _swiglu_width(W, "x")
+    if x.shape[0] > 1 and _rows(x, "x") % 8:
+        raise ValueError("silu_mul_quant: the row stride of x must be a multiple of 8 elements")
     q = torch.empty((M, F), device=x.device, dtype=E4M3)
     s = torch.empty((M, 1), device=x.device, dtype=torch.float32)
     _lib.call("h3fp8_silu_mul_quant", x.data_ptr(), _rows(x, "x"), M, F, q.data_ptr(), F, s.data_ptr(), _stream(x))
@@ -509,7 +583,7 @@ def scale_bias_cast(x32: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias:
                     out_dtype: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:
     """The two-pass scale pass: round(sa * (sb * x32)) (+ bias by one fma) (h3_tp2/fp8_gemm.py:37-54, :167-171)."""
     _need_cuda(x32, sa, sb)
-    M, N = x32.shape
+    M, N = _product_in(x32)
     s_a, sa_st, s_b, sb_st = _epi_scales(x32, sa, sb, N)
     if out_dtype not in (torch.bfloat16, torch.float16):
         raise ValueError(f"scale_bias_cast writes bf16 or fp16, got {out_dtype}")

@@ -66,9 +66,12 @@ def _fake_upstream():
     tr.fused_qk_norm_rope, tr.indexed_gate = _qk, _indexed_gate
     tr.indexed_gate_rms_norm_scale_shift, tr.rms_norm_indexed_scale_shift = _gate_rms, _rms
     qk = types.SimpleNamespace(_rms_norm_rope_kernel=_kernel, _launch_fused_rms_norm_rope=_launcher,
-                               _fused_qk_norm_rope_impl=_launcher, _fused_cuda_supported=_launcher)
+                               _fused_qk_norm_rope_impl=_launcher, _fused_cuda_supported=_launcher,
+                               fused_qk_norm_rope=_qk)
     im = types.SimpleNamespace(_indexed_gate_kernel=_kernel, _indexed_gate_rms_norm_scale_shift_kernel=_kernel,
-                               _rms_norm_indexed_scale_shift_kernel=_kernel, _launch_row_chunks=_launcher)
+                               _rms_norm_indexed_scale_shift_kernel=_kernel, _launch_row_chunks=_launcher,
+                               indexed_gate=_indexed_gate, indexed_gate_rms_norm_scale_shift=_gate_rms,
+                               rms_norm_indexed_scale_shift=_rms)
     act = types.SimpleNamespace(SiluAndMul=type("SiluAndMul", (), {"forward_cuda": _launcher}))
     linear = types.SimpleNamespace(ColumnParallelLinear=type("C", (), {"forward": _launcher}),
                                    RowParallelLinear=type("R", (), {"forward": _launcher}))
@@ -96,7 +99,7 @@ def test_a_changed_function_skips_exactly_the_sites_that_need_it(notes, caplog):
 
     def _indexed_gate_v2(x, gate, other, indices):
         return x + 0
-    tr.indexed_gate = _indexed_gate_v2                       # upstream changed fc2's consumer
+    tr.indexed_gate = modules["im"].indexed_gate = _indexed_gate_v2     # upstream changed fc2's consumer
     assert _drift.keep_sites("consumers", ("qkv", "out", "fc2"), tr, notes, reviewed, modules) == ("qkv", "out")
     assert "site fc2 skipped" in caplog.text and "indexed_gate:" in caplog.text
 
@@ -115,13 +118,43 @@ def test_a_missing_function_skips_the_site(notes, caplog):
     assert _drift.keep_sites("consumers", ("qkv", "out", "fc2"), tr, notes, reviewed, modules) == ("qkv",)
 
 
-def test_wrappers_with_wraps_are_seen_through_foreign_ones_are_drift(notes):
+def test_method_wrappers_are_seen_through(notes):
+    """As in the reference, a method's source is read through functools.wraps (inspect unwraps it)."""
     tr, modules, reviewed = _fake_upstream()
     tr.MiniMaxH3DiTBlock.forward = functools.wraps(_block_forward)(lambda self, x: _block_forward(self, x))
     assert _drift.keep_sites("consumers", ("qkv",), tr, notes, reviewed, modules) == ("qkv",)
 
-    def foreign(x, gate, other, indices):                     # a wrapper that does not say what it wraps
+
+@pytest.mark.parametrize("with_wraps", [False, True])
+def test_a_foreign_wrapper_of_a_by_name_binding_is_drift(notes, caplog, with_wraps):
+    """The transformer must call the upstream function itself (h3_tp2/fp8_consumers.py:849-855): a wrapper someone
+    else put there -- even one made with functools.wraps, whose source reads as the upstream function's -- leaves the
+    site stock, since the fused consumer would replace the call and drop the wrapper's behaviour."""
+    tr, modules, reviewed = _fake_upstream()
+
+    def foreign(x, gate, other, indices):
         return _indexed_gate(x, gate, other, indices)
+    tr.indexed_gate = functools.wraps(_indexed_gate)(foreign) if with_wraps else foreign
+    assert _drift.keep_sites("consumers", ("qkv", "fc2"), tr, notes, reviewed, modules) == ("qkv",)
+    assert "indexed_gate: wrapped" in caplog.text
+
+
+def test_this_librarys_own_wrappers_are_seen_through(notes):
+    """A binding that is this library's wrapper of the upstream function (code in this package, an _h3_tp2_amd*
+    marker, __wrapped__) is accepted, also nested; the same marker copied onto a foreign wrapper by functools.wraps is
+    not enough (its code lives elsewhere)."""
+    tr, modules, reviewed = _fake_upstream()
+    own = fp8_consumers.make_consumer_wrapper("fc2", _indexed_gate)
+    assert _drift.is_own_wrapper(own) and own.__wrapped__ is _indexed_gate
+    tr.indexed_gate = own
+    assert _drift.keep_sites("consumers", ("fc2",), tr, notes, reviewed, modules) == ("fc2",)
+    tr.indexed_gate = fp8_consumers.make_consumer_wrapper("fc2", own)
+    assert _drift.keep_sites("consumers", ("fc2",), tr, notes, reviewed, modules) == ("fc2",)
+
+    def foreign(*args):
+        return own(*args)
+    foreign = functools.wraps(own)(foreign)                  # copies own's marker and sets __wrapped__ = own
+    assert not _drift.is_own_wrapper(foreign)
     tr.indexed_gate = foreign
     assert _drift.keep_sites("consumers", ("fc2",), tr, notes, reviewed, modules) == ()
 

@@ -137,3 +137,37 @@ def test_scale_pass_and_consumer_outputs(calls):
         ops.scale_indexed_gate(x32, torch.ones(8), torch.ones(32), None, x, gate, idx,
                                out=torch.empty(8, 32, dtype=torch.float16))
     assert calls == ["h3fp8_scale_bias_cast", "h3fp8_scale_indexed_gate"]
+
+
+def test_swiglu_passes_input_dtype_width_and_bias(calls):
+    """scale_swiglu / scale_swiglu_quant read an fp32 [M, 2F] product and a bf16 [2F] bias; silu_mul_quant reads bf16
+    [M, 2F].  A wrong input dtype (a bf16 product would be read as fp32: twice its allocation), an odd width or a width
+    whose F is not a multiple of 4, and a bias of the wrong dtype or length raise before any launch."""
+    x32 = torch.zeros(8, 64)
+    sa, sb = torch.ones(8), torch.ones(64)
+    ops.scale_swiglu(x32, sa, sb, torch.zeros(64, dtype=BF16))
+    ops.scale_swiglu_quant(x32, sa, sb, torch.zeros(64, dtype=BF16))
+    ops.silu_mul_quant(torch.zeros(8, 64, dtype=BF16))
+    assert calls == ["h3fp8_scale_swiglu", "h3fp8_scale_swiglu_quant", "h3fp8_silu_mul_quant"]
+    for fn in (ops.scale_swiglu, ops.scale_swiglu_quant):
+        for x in (torch.zeros(8, 64, dtype=BF16),             # a bf16 "product"
+                  torch.zeros(8, 64, dtype=torch.float64),
+                  torch.zeros(8, 63),                          # odd width
+                  torch.zeros(8, 68),                          # F = 34, not a multiple of 4
+                  torch.zeros(64, 8).t(),                      # rows not contiguous
+                  torch.zeros(8, 2, 32)):                      # not 2-D
+            with pytest.raises(ValueError):
+                fn(x, sa, torch.ones(x.shape[-1]) if x.dim() == 2 else sb)
+        for bias in (torch.zeros(32, dtype=BF16),             # [F]: the kernels read 2F entries
+                     torch.zeros(64),                          # fp32
+                     torch.zeros(64, dtype=torch.float16),
+                     torch.zeros(128, dtype=BF16)[::2]):
+            with pytest.raises(ValueError):
+                fn(x32, sa, sb, bias)
+    for x in (torch.zeros(8, 64), torch.zeros(8, 64, dtype=torch.float16), torch.zeros(8, 63, dtype=BF16),
+              torch.zeros(8, 68, dtype=BF16), torch.zeros(8, 68, dtype=BF16)[:, :64], torch.zeros(64, dtype=BF16)):
+        with pytest.raises(ValueError):
+            ops.silu_mul_quant(x)
+    with pytest.raises(ValueError):
+        ops.scale_bias_cast(torch.zeros(8, 32, dtype=BF16), torch.ones(8), torch.ones(32), None, BF16)
+    assert calls == ["h3fp8_scale_swiglu", "h3fp8_scale_swiglu_quant", "h3fp8_silu_mul_quant"]

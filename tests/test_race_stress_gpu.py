@@ -1,5 +1,8 @@
 """Race stress of the GEMM kernels' hand-rolled stage release (fence-free barriers with explicit vmcnt / lgkmcnt waits):
-kernel 2 at the 960x576 QKV shape and kernel 3 at the 1344x768 FFN gate/up shape, launched again and again while a
+kernel 2 at the 960x576 QKV shape (full tiles with the half-tile tail), kernel 3 at the 1344x768 FFN gate/up shape,
+the single linear 2048 x 3072 x 3072 (the 128 x 192 tiles: a three-stage ring with one barrier per k-step) and the
+M = 2 adaLN GEMM 2 x 3072 -> 18 432 (the small-M form: a per-wave LDS ring released by its own vmcnt / lgkmcnt waits
+alone), launched again and again while a
 memory-bound co-runner (a 1 GiB device-to-device copy) runs on a second stream of the same (default) priority, so that
 the persistent workgroups meet unpredictable memory latencies and CU sharing.  Every output must equal the first one
 bit for bit (and the first must equal a launch with no co-runner).  The loop stops at the first mismatch and is
@@ -29,25 +32,33 @@ def _operands(device):
     w2, sw2 = ops.quant_rows(synthetic.weight(N2, K, seed=1).to(device))
     a3, s3 = ops.quant_rows(synthetic.activations(M3, K, seed=2, n_out=3).to(device))
     w3, sw3 = ops.quant_rows(synthetic.weight(2 * F, K, seed=3).to(device))
-    return (a2, w2, s2, sw2.view(-1)), (a3, w3, s3, sw3.view(-1))
+    a1, s1 = ops.quant_rows(synthetic.activations(2048, K, seed=4, n_out=8).to(device))
+    w1, sw1 = ops.quant_rows(synthetic.weight(K, K, seed=5).to(device))
+    a4, s4 = ops.quant_rows(synthetic.activations(2, K, seed=6, n_out=3).to(device))
+    w4, sw4 = ops.quant_rows(synthetic.weight(6 * K, K, seed=7).to(device))
+    return ((a2, w2, s2, sw2.view(-1)), (a3, w3, s3, sw3.view(-1)), (a1, w1, s1, sw1.view(-1)),
+            (a4, w4, s4, sw4.view(-1)))
 
 
 def run(seconds: float, device, log=print) -> dict:
-    """Alternate kernel 2 and kernel 3 launches under the co-runner for ``seconds``; returns counts, raises
+    """Alternate the kernel-2 forms and kernel 3 under the co-runner for ``seconds``; returns counts, raises
     AssertionError at the first output that differs from the first launch's."""
     from h3_tp2_amd import ops
-    (a2, w2, s2, sw2), (a3, w3, s3, sw3) = _operands(device)
+    (a2, w2, s2, sw2), (a3, w3, s3, sw3), (a1, w1, s1, sw1), (a4, w4, s4, sw4) = _operands(device)
     amax3 = torch.empty(a3.shape[0], device=device)
     ref2 = ops.gemm(a2, w2, s2, sw2)
     ref3 = ops.gemm_swiglu(a3, w3, s3, sw3, row_amax=amax3)
     ref_amax3 = amax3.clone()
+    ref1 = ops.gemm(a1, w1, s1, sw1)                        # 256 tiles of 128 x 192
+    ref4 = ops.gemm(a4, w4, s4, sw4)                        # the small-M form
+    out1, out4 = torch.empty_like(ref1), torch.empty_like(ref4)
     torch.cuda.synchronize()
     src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(3)
     dst = torch.empty_like(src)
     side = torch.cuda.Stream(device=device)                 # default priority, like the launch stream
     main = torch.cuda.current_stream(device)
     out2, out3 = torch.empty_like(ref2), torch.empty_like(ref3)
-    counts = {"kernel2": 0, "kernel3": 0, "co_runner_copies": 0}
+    counts = {"kernel2": 0, "kernel3": 0, "w192": 0, "small_m": 0, "co_runner_copies": 0}
     t_end = time.time() + seconds
     while time.time() < t_end:
         side.wait_stream(main)
@@ -57,16 +68,21 @@ def run(seconds: float, device, log=print) -> dict:
         counts["co_runner_copies"] += 3
         ops.gemm(a2, w2, s2, sw2, out=out2)
         ops.gemm_swiglu(a3, w3, s3, sw3, row_amax=amax3, out=out3)
+        for _ in range(4):                                  # the short launches, several times per round
+            ops.gemm(a1, w1, s1, sw1, out=out1)
+            ops.gemm(a4, w4, s4, sw4, out=out4)
         main.wait_stream(side)
-        ok2 = torch.equal(out2.view(torch.int16), ref2.view(torch.int16))
-        ok3 = torch.equal(out3.view(torch.int16), ref3.view(torch.int16)) and torch.equal(amax3, ref_amax3)
-        counts["kernel2"] += 1
-        counts["kernel3"] += 1
-        if not (ok2 and ok3):
-            bad2 = int((out2.view(torch.int16) != ref2.view(torch.int16)).sum())
-            bad3 = int((out3.view(torch.int16) != ref3.view(torch.int16)).sum())
-            raise AssertionError(f"output differs from the first launch after {counts}: kernel 2 {bad2} elements, "
-                                 f"kernel 3 {bad3} elements")
+        same = {"kernel2": torch.equal(out2.view(torch.int16), ref2.view(torch.int16)),
+                "kernel3": torch.equal(out3.view(torch.int16), ref3.view(torch.int16)) and torch.equal(amax3, ref_amax3),
+                "w192": torch.equal(out1.view(torch.int16), ref1.view(torch.int16)),
+                "small_m": torch.equal(out4.view(torch.int16), ref4.view(torch.int16))}
+        for k in same:
+            counts[k] += 1 if k in ("kernel2", "kernel3") else 4
+        if not all(same.values()):
+            bad = {k: int((o.view(torch.int16) != r.view(torch.int16)).sum())
+                   for k, o, r in (("kernel2", out2, ref2), ("kernel3", out3, ref3), ("w192", out1, ref1),
+                                   ("small_m", out4, ref4))}
+            raise AssertionError(f"output differs from the first launch after {counts}: differing elements {bad}")
         if counts["kernel2"] % 25 == 0:
             log(f"race stress: {counts} equal so far", flush=True)
     torch.cuda.synchronize()
@@ -75,7 +91,7 @@ def run(seconds: float, device, log=print) -> dict:
 
 def test_gemm_stage_release_under_a_co_runner(cuda):
     counts = run(SECONDS, cuda)
-    assert counts["kernel2"] >= 5 and counts["kernel3"] >= 5
+    assert counts["kernel2"] >= 5 and counts["kernel3"] >= 5 and counts["w192"] >= 20 and counts["small_m"] >= 20
 
 
 if __name__ == "__main__":

@@ -78,3 +78,30 @@ def test_noalloc_at_the_row_limit_and_refusals(cuda):
     assert L.h3fp8_gemm_quant_noalloc(None, 32, None, 32, None, 1, None, 1, None, None, 32, 4, 24, 24, dummy, 32,
                                       dummy, None) == -22
     assert b"multiples of 16" in L.h3fp8_last_error()
+
+
+def test_noalloc_captured_in_a_graph_replays_bitwise(cuda):
+    """The entry point captured in a HIP graph (torch.cuda.graph): the row maxima are cleared by a fill kernel, so no
+    memset node is recorded.  Three replays, each after the outputs were overwritten eagerly and other eager GEMM work
+    ran, with a synchronisation in between; every replay equals the workspace form bit for bit."""
+    from h3_tp2_amd import ops
+    M, N, K = 3000, 3072, 1024
+    a, w, sa, sb = serving_like(M, N, K, seed=77, device=cuda)
+    y0, q0, s0 = _outputs(M, N, cuda)
+    _call("h3fp8_gemm_quant", a, w, sa, sb, y0, q0, s0, torch.empty(M, device=cuda))
+    y1, q1, s1 = _outputs(M, N, cuda)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _call("h3fp8_gemm_quant_noalloc", a, w, sa, sb, y1, q1, s1)
+    a2, w2, sa2, sb2 = serving_like(700, 1024, 512, seed=78, device=cuda)
+    for rep in range(3):
+        y1.fill_(float("nan"))
+        q1.view(torch.uint8).fill_(0x7F)
+        s1.fill_(-1.0)
+        ops.gemm_quant(a2, w2, sa2, sb2)                    # other eager work between the replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert _same(y1, y0) and _same(q1, q0) and _same(s1, s0), f"replay {rep}"
+    del g
