@@ -489,6 +489,17 @@ def install(sites=SITES, tr=None, *, lora_types=None, fused: bool = True, check_
     if not two_pass:
         logger.warning("h3_tp2_amd fp8 consumers: needs the dispatcher's two-pass level; skipped")
         return []
+    from . import fp8_hip  # noqa: PLC0415
+    if fp8_hip.route in fp8_gemm._routers:
+        # the block router computes its sites in bf16 ahead of the stash hook, so their consumers stay stock
+        # (h3_tp2/fp8_consumers.py:870-877)
+        routed = [site for site in chosen if site in fp8_hip.SITES]
+        chosen = tuple(site for site in chosen if site not in fp8_hip.SITES)
+        if routed:
+            logger.warning("h3_tp2_amd fp8 consumers: the block router computes %s in bf16, so those consumers stay "
+                           "stock; fused sites: %s", ", ".join(routed), ", ".join(chosen) or "none")
+        if not chosen:
+            return []
     if tr is None:
         from vllm_omni.diffusion.models.minimax_h3 import minimax_h3_transformer as tr  # noqa: PLC0415
     block_cls = tr.MiniMaxH3DiTBlock

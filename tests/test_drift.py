@@ -186,3 +186,24 @@ def test_swiglu_install_checks_the_mlp_forward(monkeypatch):
         assert _drift.fingerprint(tr.MiniMaxH3MLP.forward) == reviewed["mlp_forward"]
     finally:
         fp8_gemm.clear_hooks()
+
+
+def test_consumer_install_leaves_router_sites_stock(monkeypatch, caplog):
+    """With the block router registered (the two-pass level plus kernel 2 for the block's qkv / out / fc1, the
+    reference's cutlass layout), qkv and out are computed in bf16 ahead of the stash hook: their consumers stay stock
+    and only fc2 is fused (h3_tp2/fp8_consumers.py:870-877)."""
+    monkeypatch.setitem(fp8_gemm._state, "level", "tensor32")
+    monkeypatch.setitem(fp8_gemm._state, "fused", False)
+    monkeypatch.setattr(fp8_consumers, "_state", {"sites": (), "disabled": set(), "fused": {}, "checked": {}})
+    tr, modules, reviewed = _fake_upstream()
+    from h3_tp2_amd import fp8_hip
+    caplog.set_level("WARNING")
+    try:
+        fp8_gemm.set_router(fp8_hip.route)
+        assert fp8_consumers.install(("qkv", "out", "fc2"), tr=tr, lora_types=(), reviewed=reviewed,
+                                     modules=modules) == ["fc2"]
+        assert tr.fused_qk_norm_rope is _qk and tr.indexed_gate_rms_norm_scale_shift is _gate_rms
+        assert tr.indexed_gate._h3_tp2_amd_consumer
+        assert "block router computes qkv, out" in caplog.text
+    finally:
+        fp8_gemm.clear_hooks()
