@@ -42,6 +42,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--preroll-s", type=float, default=1.0,
                     help="seconds of untimed chain steps before the warm-up (lets the chip's clock settle)")
+    ap.add_argument("--settle-s", type=float, default=0.25,
+                    help="seconds of untimed calls before each other workload's warm-up (its inputs are made on the "
+                         "host while the GPU idles, so the clock drops between workloads)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of the extra workloads to run (default: all; 'none': none)")
     ap.add_argument("--cpu-rows", type=int, default=2048, help="token rows of the CPU baseline sample")
@@ -103,8 +106,21 @@ def main() -> None:
     def ev():
         return torch.cuda.Event(enable_timing=True)
 
+    def settle(fn, seconds=None):
+        """Untimed calls for `seconds` (default --settle-s): the clock climbs back after the host-side set-up."""
+        t_a = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t_a < (args.settle_s if seconds is None else seconds) or n < 2:
+            fn()
+            n += 1
+            if n % 16 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
+
     def time_steps(fn, steps, warmup):
-        """Total time of `steps` back-to-back calls (ms), after `warmup` untimed ones; synchronised on both sides."""
+        """Total time of `steps` back-to-back calls (ms), after a clock settle and `warmup` untimed ones; synchronised
+        on both sides."""
+        settle(fn)
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -267,6 +283,7 @@ def main() -> None:
             ops.gemm(q2, w2, sq2, sw2, torch.bfloat16, out=y2)
             if m:
                 m[2].record(stream)
+        settle(c2_step)
         for _ in range(max(warm, 20)):
             c2_step()
         torch.cuda.synchronize()
@@ -281,12 +298,17 @@ def main() -> None:
         tg2 = sum(e[1].elapsed_time(e[2]) for e in ev2) / steps
         qb2 = 3.0 * M2 * K2 + 4.0 * M2
         if want("c2"):
+            # the quant alone, 4 x steps back-to-back launches: a 26 us kernel bracketed by events inside the step
+            # (quant_ms) carries the events' own cost; back to back it carries only the gap between launches
+            tqb = time_steps(lambda: ops.quant_rows(x2, q2, sq2), 4 * steps, warm) / (4 * steps)
             out["c2_qkv_960x576_5s"] = {
                 "ms_per_step": round(t2, 4), "TFLOP/s": round(tflops(f2, t2), 1),
                 "kernel2_ms": round(tg2, 4), "kernel2_TFLOP/s": round(tflops(f2, tg2), 1),
                 "kernel2_frac_mfma": round(tflops(f2, tg2) / PEAK_TFLOPS, 4),
                 "quant_ms": round(tq2, 4), "quant_GB/s": round(gbs(qb2, tq2), 1),
                 "quant_frac_hbm": round(gbs(qb2, tq2) / PEAK_GBS, 4),
+                "quant_back_to_back": {"ms": round(tqb, 4), "GB/s": round(gbs(qb2, tqb), 1),
+                                       "frac_hbm": round(gbs(qb2, tqb) / PEAK_GBS, 4)},
                 "step_minus_launches_ms": round(t2 - tq2 - tg2, 4)}
         if want("vendor"):
             # The same GEMM through the vendor library (torch._scaled_mm -> hipBLASLt) on the same fp8 operands and
@@ -423,6 +445,7 @@ def main() -> None:
                 launches.append((name, (lambda a_=ah, w_=wh, s_=sah, t_=swh, y_=yh:
                                         ops.gemm(a_, w_, s_, t_, torch.bfloat16, out=y_)), 2.0 * Mh * Nh * Kh, 0.0))
         hsteps = max(5, steps // 3)
+        settle(lambda: [fn() for _, fn, _, _ in launches])
         for _ in range(3):
             for _, fn, _, _ in launches:
                 fn()

@@ -255,6 +255,13 @@ __device__ __forceinline__ void mfma_one(v16f acc[4][4], const v8i af[4], const 
                                                                          0, 0, 0, 0);
 }
 
+// The first MFMA of an accumulator block in a tile: C is the inline constant 0, so the 256 accumulators of a tile
+// are never cleared by moves.
+__device__ __forceinline__ void mfma_zero(v16f acc[4][4], const v8i af[4], const v8i bf[4], int t) {
+    const v16f z = {};
+    acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[t >> 2], bf[t & 3], z, 0, 0, 0, 0, 0, 0);
+}
+
 struct GroupedParams {
     GemmParams g[H3FP8_MAX_GROUPS];
     int n;
@@ -436,7 +443,8 @@ constexpr int ks_loads_before_pub() {
     return stage + (KS_REL + 9 <= KS_PUB ? 2 : 0);
 }
 
-template <int EPI, bool READ_NEXT>
+// FIRST: the tile's first k-step, whose sub-step-0 MFMAs start their accumulator blocks from 0.
+template <int EPI, bool READ_NEXT, bool FIRST>
 __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const Cursor& I, uint32_t wofs, int wn, int wm,
                                       int lane, v16f acc[4][4], v8i fa0[4], v8i fb0[4], v8i fa1[4], v8i fb1[4]) {
     uint8_t* cur = lds + (g & 1) * STAGE_BYTES;
@@ -446,8 +454,12 @@ __device__ __forceinline__ void kstep(uint8_t* lds, uint32_t lds0, int g, const 
     constexpr int PER = (8 + NREAD - 1) / NREAD;
 #pragma unroll
     for (int u = 0; u < 32; ++u) {
-        if (u < 16) mfma_one(acc, fa0, fb0, u);
-        else mfma_one(acc, fa1, fb1, u - 16);
+        if (u < 16) {
+            if (FIRST) mfma_zero(acc, fa0, fb0, u);
+            else mfma_one(acc, fa0, fb0, u);
+        } else {
+            mfma_one(acc, fa1, fb1, u - 16);
+        }
         if (u < 8) read_one<EPI>(cur, wn, wm, lane, 1, u, fa1, fb1);
         if (u == KS_REL) {
             wait_lgkm0();                               // this wave's reads of stage g & 1 have returned
@@ -714,7 +726,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
         }
     } else {
         const int col0 = wcol;
-        // every scale the wave needs, read once up front (one LDS round trip instead of one per group of four)
+        // the wave's token scales, and with the row maximum or a bias its channel scales too, read once up front (one
+        // LDS round trip instead of one per group of four); the plain epilogue reads each group's channel scales where
+        // it uses them, which leaves it the registers to run without scratch
+        constexpr bool SB_UPFRONT = EPI == EPI_AMAX || HAS_BIAS;
         float sa_j[4];
         v4f sb_v[4][4];
 #pragma unroll
@@ -722,7 +737,8 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sb_v[i][q] = *reinterpret_cast<const v4f*>(sb_l + wsb + 32 * i + 8 * q + 4 * hi);
+            for (int q = 0; q < 4; ++q)
+                if (SB_UPFRONT) sb_v[i][q] = *reinterpret_cast<const v4f*>(sb_l + wsb + 32 * i + 8 * q + 4 * hi);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = mrow0 + 32 * j + mj;
@@ -741,7 +757,8 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                         const int cl = 32 * ii + 8 * q + 4 * hi;          // column within the 64-wide pass
                         const int n = col0 + 64 * ip + cl;
                         const bool ok = n < p.N && m < p.M;
-                        const v4f sbn = sb_v[i][q];
+                        const v4f sbn = SB_UPFRONT ? sb_v[i][q]
+                                                   : *reinterpret_cast<const v4f*>(sb_l + wsb + 32 * i + 8 * q + 4 * hi);
                         float bn[4] = {0, 0, 0, 0};
                         if (HAS_BIAS) {                 // columns past N read column 0 (not stored)
                             const int nc = n < p.N ? n : 0;
@@ -825,20 +842,29 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
         const int nk = (p.K + BK - 1) / BK;
 
         v16f acc[4][4];
+        int ks = 0;
+        if (OUT_DT != H3FP8_DT_F32 && nk > 1) {
+            // the first k-step's MFMAs start every accumulator block from 0 (the raw-accumulator probe, a test form,
+            // clears instead: it keeps its registers clear of scratch that way)
+            kstep<EPI, true, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+            if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
+            ++g;
+            ++ks;
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-        for (int ks = 0; ks < nk - 1; ++ks, ++g) {
-            kstep<EPI, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        }
+        for (; ks < nk - 1; ++ks, ++g) {
+            kstep<EPI, true, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
             if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
         }
         // the tile's last k-step publishes the next k-step's stage but leaves its fragment registers free for the
         // epilogue; they are read after it
-        kstep<EPI, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
+        kstep<EPI, false, false>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
         if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
         ++g;
         epilogue<OUT_DT, HAS_BIAS, EPI>(p, tm, tn, lds, c % NSCALE, wave, wn, wm, lane, acc);
