@@ -14,9 +14,10 @@ against the 5.0 PFLOP/s FP8 dense MFMA peak.  Before the warm-up steps an explic
 ``--preroll-s`` seconds: the chip's clock moves over the first heavy calls, and the pre-roll makes the timed steps
 independent of how short the warm-up is.  The other measured workloads (the QKV projection at 960x576, the single
 linear, the FFN at 1344x768 5 s, the grouped launch, the reference's four H3 linears at its per-rank M = 42 848, the
-host cost of one dispatched call, the producers / consumers passes, the vendor GEMM) are reported under
-``workloads``.  ``cpu_baseline`` times the reference's torch CPU path (oracle/torch_path.py) of the same chain on
-a row sample, on this host's cores.  Synthetic seeded inputs, random-init weights (no checkpoints).
+host cost of one dispatched call, the producers / consumers passes, the vendor GEMM, the socket power and clock of
+each chain launch beside a register-only MFMA loop) are reported under ``workloads``.  ``cpu_baseline`` times the
+reference's torch CPU path (oracle/torch_path.py) of the same chain on a row sample, on this host's cores.  Synthetic
+seeded inputs, random-init weights (no checkpoints).
 """
 from __future__ import annotations
 
@@ -51,7 +52,19 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU baseline for at least this long")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 512 MiB device-to-device copy (the known-size kernel that scales PMC byte counts)")
+    ap.add_argument("--power-s", type=float, default=2.0,
+                    help="seconds each launch of the power / clock workload runs back to back")
     return ap.parse_args()
+
+
+def smi_sample(smi: str) -> tuple[float, float]:
+    """(socket power W, mean gfx clock MHz over the XCDs) of GPU 0 from one `amd-smi metric -p -c --json` call."""
+    r = subprocess.run([smi, "metric", "-p", "-c", "--json"], capture_output=True, text=True, timeout=10)
+    o = json.loads(r.stdout)
+    g = o["gpu_data"][0] if isinstance(o, dict) else o[0]
+    clks = [float(v["clk"]["value"]) for k, v in g["clock"].items()
+            if k.startswith("gfx_") and isinstance(v, dict) and isinstance(v.get("clk"), dict)]
+    return float(g["power"]["socket_power"]["value"]), sum(clks) / len(clks)
 
 
 def host_cpu() -> dict:
@@ -255,11 +268,80 @@ def main() -> None:
                "step_minus_launches_ms": round(t_step - sum(seg_ms), 4),
                "note": "out-proj input is a seeded bf16 stand-in for the attention output; value counts the four "
                        "GEMMs' FLOPs over the whole step (quant and tail passes included in the time)"}
+    def want(name):
+        return "none" not in only and (not only or name in only)
+
+    if want("power"):
+        # Socket power and gfx clock while each launch of the chain runs back to back for --power-s seconds, beside
+        # the register-only MFMA loop (the chip's sustained FP8 MFMA rate with no memory traffic): the FP8 GEMMs run
+        # at the 1400 W board limit, where the clock, not the schedule, sets the MFMA rate.
+        import shutil
+        import threading
+        smi = shutil.which("amd-smi")
+        if smi is None:
+            out["power_clock"] = {"skipped": "amd-smi not found"}
+        else:
+            samples, stop = [], []
+
+            def sampler():
+                while not stop:
+                    t_s = time.time()
+                    try:
+                        samples.append((t_s,) + smi_sample(smi))
+                    except Exception:                   # a missed sample only thins the window
+                        pass
+                    time.sleep(0.2)
+
+            ml_out = torch.empty(256 * 256, device=dev, dtype=torch.float32)
+            ml_iters = 10000
+            legs = [("mfma_register_loop (no memory traffic)", lambda: ops.mfma_loop(ml_out, ml_iters),
+                     ops.MFMA_LOOP_FLOP_PER_ROUND * 256 * ml_iters, 0.0)]
+            legs += [seg[i] for i in (1, 3, IDX_K3, 7, 0)]
+            th = threading.Thread(target=sampler, daemon=True)
+            th.start()
+            pw = {}
+            ceiling = None
+            for name, fn, f, b in legs:
+                fn()
+                torch.cuda.synchronize()
+                e0, e1 = ev(), ev()
+                t_a = time.time()
+                n = 0
+                e0.record(stream)
+                while time.time() - t_a < args.power_s:
+                    for _ in range(4):
+                        fn()
+                    n += 4
+                    torch.cuda.synchronize()
+                e1.record(stream)
+                e1.synchronize()
+                t_b = time.time()
+                ms = e0.elapsed_time(e1) / n
+                win = sorted((p, c) for t_s, p, c in samples if t_a + 0.6 <= t_s <= t_b)
+                e = {"ms": round(ms, 4), "samples": len(win)}
+                if win:
+                    e["socket_power_W"] = win[len(win) // 2][0]
+                    e["gfx_clock_MHz"] = round(sorted(c for _, c in win)[len(win) // 2])
+                if f:
+                    e["TFLOP/s"] = round(tflops(f, ms), 1)
+                    e["frac_mfma"] = round(tflops(f, ms) / PEAK_TFLOPS, 4)
+                    if ceiling is None:
+                        ceiling = tflops(f, ms)
+                    else:
+                        e["frac_of_register_loop"] = round(tflops(f, ms) / ceiling, 4)
+                else:
+                    e["GB/s"] = round(gbs(b, ms), 1)
+                    e["frac_hbm"] = round(gbs(b, ms) / PEAK_GBS, 4)
+                pw[name] = e
+            stop.append(True)
+            th.join()
+            pw["note"] = ("median socket power and gfx clock (amd-smi, every ~0.3 s) over each back-to-back run after "
+                          "its first 0.6 s; the 5.0 PFLOP/s peak is quoted at the 2.4 GHz maximum clock")
+            out["power_clock"] = pw
+            del ml_out
     del x4, xo, yqkv, hws, y_out, y_d, q0, qo, qg, qh, qn
 
     # ---- the other measured workloads ----
-    def want(name):
-        return "none" not in only and (not only or name in only)
 
     if want("c2") or want("vendor"):
         # The QKV projection at the 5 s 960x576 token count (M = 31 x 540): quant of X + kernel 2, with the two

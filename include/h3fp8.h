@@ -277,6 +277,14 @@ int h3fp8_selfcheck_e4m3(uint64_t* mismatches, uint64_t* nan_bad);
 int h3fp8_selfcheck_bf16(uint64_t* mismatches, uint64_t* nan_bad);
 int h3fp8_copy_silu_table(void* out, void* stream);
 
+/*
+ * Measurement (no counterpart in the reference): the sustained FP8 MFMA rate of the chip with no memory traffic.
+ * `blocks` workgroups of 4 waves each run `iters` rounds of 16 independent v_mfma 32x32x64 e4m3 MFMAs on register
+ * operands (the GEMM's per-wave accumulator block), 2 * 32 * 32 * 64 * 16 * 4 * iters * blocks FLOP per launch.
+ * `out` (device, blocks * 256 floats) receives one sum per thread.  blocks in [1, 65535], iters in [1, 2^30].
+ */
+int h3fp8_mfma_loop(float* out, int64_t blocks, int64_t iters, uint32_t seed, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

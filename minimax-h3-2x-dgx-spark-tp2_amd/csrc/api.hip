@@ -59,6 +59,56 @@ __global__ void __launch_bounds__(256) h3_build_silu_table_kernel() {
     g_h3_silu_table[i] = (uint16_t)r;
 }
 
+// The chip's sustained FP8 MFMA rate with no memory traffic: each wave keeps the GEMM's 4 x 4 block of 32x32x64 e4m3
+// accumulators and issues 16 independent MFMAs per round, two of its eight operand registers changing between rounds
+// (finite e4m3 bytes with random signs, so the multipliers toggle as on real data).  One store per thread at the end
+// keeps the work.  It runs at the clock the chip holds under FP8 MFMA load, which is what bounds the GEMMs beside
+// the published peak.
+__global__ void __launch_bounds__(256, 1) h3_mfma_loop_kernel(float* out, int iters, uint32_t seed) {
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    using h3::v8i;
+    const int lane = threadIdx.x & 63;
+    v8i af[4], bf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint32_t x = (uint32_t)lane * 2654435761u ^ (uint32_t)(i * 8 + e) * 40503u ^ seed;
+            x ^= x >> 13;
+            x *= 0x5bd1e995u;
+            x ^= x >> 15;
+            af[i][e] = (int)(x & 0xbebebebeu);          // bytes below 0x7f in magnitude: finite e4m3
+            uint32_t y = x * 0x27d4eb2du;
+            y ^= y >> 16;
+            bf[i][e] = (int)(y & 0xbebebebeu);
+        }
+    v16f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v16f){};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+            acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[t >> 2], bf[t & 3],
+                                                                                 acc[t >> 2][t & 3], 0, 0, 0, 0, 0, 0);
+        const int m = (it * 0x01030507) & 0x3e3e3e3e;   // flips low bits of each byte: finite stays finite
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            af[0][e] ^= m;
+            bf[1][e] ^= m;
+        }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s += acc[i][j][r];
+    out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 __global__ void __launch_bounds__(256) h3_build_silu_rot_kernel() {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= H3_SILU_ROT_LEN) return;
@@ -194,6 +244,16 @@ int h3fp8_selfcheck_bf16(uint64_t* mismatches, uint64_t* nan_bad) {
     H3_CHECK_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(g_h3_cvt_counts), sizeof(out)));
     *mismatches = out[2];
     *nan_bad = out[3];
+    return H3FP8_OK;
+}
+
+int h3fp8_mfma_loop(float* out, int64_t blocks, int64_t iters, uint32_t seed, void* stream) {
+    H3_REQUIRE(out, "h3fp8_mfma_loop: null output");
+    H3_REQUIRE(blocks >= 1 && blocks <= 65535 && iters >= 1 && iters <= (1 << 30),
+               "h3fp8_mfma_loop: blocks must be in [1, 65535] and iters in [1, 2^30]");
+    hipLaunchKernelGGL(h3_mfma_loop_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, out, (int)iters,
+                       seed);
+    H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
 

@@ -64,6 +64,7 @@ _SIGS = {
     "h3fp8_selfcheck_e4m3": ([ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], I),
     "h3fp8_selfcheck_bf16": ([ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], I),
     "h3fp8_copy_silu_table": ([P, P], I),
+    "h3fp8_mfma_loop": ([P, I64, I64, ctypes.c_uint32, P], I),
 }
 
 EXPORTS = tuple(_SIGS)

@@ -644,3 +644,17 @@ def silu_table(device=None) -> torch.Tensor:  # noqa: ANN001
     with torch.cuda.device(dev):
         _lib.call("h3fp8_copy_silu_table", out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
     return out
+
+
+MFMA_LOOP_FLOP_PER_ROUND = 2.0 * 32 * 32 * 64 * 16 * 4    # per workgroup and round of h3fp8_mfma_loop
+
+
+def mfma_loop(out: torch.Tensor, iters: int, seed: int = 1) -> float:
+    """Launches the register-only FP8 MFMA loop (one workgroup per 256 floats of ``out``, ``iters`` rounds) on the
+    current stream and returns its FLOP count: the chip's sustained MFMA rate with no memory traffic."""
+    _need_cuda(out)
+    if out.dtype != torch.float32 or not out.is_contiguous() or out.numel() % 256 or out.numel() == 0:
+        raise ValueError("out must be a contiguous fp32 tensor of a positive multiple of 256 elements")
+    blocks = out.numel() // 256
+    _lib.call("h3fp8_mfma_loop", out.data_ptr(), blocks, int(iters), int(seed) & 0xffffffff, _stream(out))
+    return MFMA_LOOP_FLOP_PER_ROUND * blocks * iters

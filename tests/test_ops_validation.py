@@ -171,3 +171,14 @@ def test_swiglu_passes_input_dtype_width_and_bias(calls):
     with pytest.raises(ValueError):
         ops.scale_bias_cast(torch.zeros(8, 32, dtype=BF16), torch.ones(8), torch.ones(32), None, BF16)
     assert calls == ["h3fp8_scale_swiglu", "h3fp8_scale_swiglu_quant", "h3fp8_silu_mul_quant"]
+
+
+def test_mfma_loop_output(calls):
+    """The measurement loop writes one float per thread of 256-thread workgroups: its output must be a contiguous
+    fp32 tensor of a positive multiple of 256 elements; the FLOP count follows the workgroups and rounds."""
+    assert ops.mfma_loop(torch.empty(512), 3) == 2.0 * 32 * 32 * 64 * 16 * 4 * 2 * 3
+    assert calls == ["h3fp8_mfma_loop"]
+    for out in (torch.empty(300), torch.empty(0), torch.empty(512, dtype=torch.float16), torch.empty(1024)[::2]):
+        with pytest.raises(ValueError):
+            ops.mfma_loop(out, 3)
+    assert calls == ["h3fp8_mfma_loop"]
