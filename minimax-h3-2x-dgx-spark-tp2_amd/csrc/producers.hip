@@ -320,8 +320,9 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
     });
 }
 
-// The producers and the out consumer with their tables staged in LDS as fp32: eight rows per 512-thread workgroup,
-// one wave per row.  The modulation tables have one row per sample, so nearly every workgroup's rows share one index:
+// The producers and the out consumer with their tables staged in LDS as fp32: one wave per row, eight rows per
+// workgroup for the gated forms and four for the qkv producer (measured: with eight rows its index-run case took
+// 2 % and its random-index case 14 % longer, and the out consumer 14 % longer with four).  The modulation tables have one row per sample, so nearly every workgroup's rows share one index:
 // the workgroup converts once into fp32 LDS tables the weight row, 1 + scale and shift of its first row's index, and
 // for the gated forms gate of that index, for the fp32-branch form sb and the bias (the same fp32 values the
 // per-element arithmetic forms: bf16 -> fp32 is exact, 1 + scale the same fp32 add).  A wave whose row has that index
@@ -332,11 +333,15 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
 // LDS: table t, half s (elements 0-3 / 4-7 of a chunk), chunk c: tabs[t][s][c] (float4), so a wave's 16-byte reads
 // of one half are contiguous (no bank conflicts).  Tables: T_W weight, T_G 1 + scale, T_B shift, T_GATE gate,
 // T_SB sb, T_BIAS bias (zeros without one).
+template <bool GATE>
+constexpr int staged_rows() { return GATE ? 8 : 4; }
+
 template <bool GATE, bool B32, int OUT, int CPL, bool FULL>
-__global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
+__global__ void __launch_bounds__(64 * staged_rows<GATE>()) rms_mod_quant_staged_kernel(RmsArgs a) {
     constexpr bool QUANT = (OUT & 1) != 0, WRITE_H = (OUT & 2) != 0;
+    constexpr int ROWS = staged_rows<GATE>(), THREADS = 64 * ROWS;
     constexpr int NC = 64 * CPL;                        // 16-byte bf16 chunks per table row (past H: zeros)
-    static_assert(NC <= 512, "one staging load per thread and table");
+    static_assert(NC <= 2 * THREADS, "at most two staging loads per thread and table");
     static_assert(GATE || !B32, "the fp32 branch belongs to the gated form");
     constexpr int T_W = 0, T_G = 1, T_B = 2, T_GATE = 3, T_SB = GATE ? 4 : 3, T_BIAS = T_SB + 1;
     // a wave off the staged index loads its tables in groups of FB_GROUP chunks (one chunk at a time for the qkv
@@ -346,7 +351,7 @@ __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
     __shared__ v4f tabs[NT][2][NC];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t m0 = (int64_t)blockIdx.x * 8, m = m0 + wave;
+    const int64_t m0 = (int64_t)blockIdx.x * ROWS, m = m0 + wave;
     const bool live = m < a.M;
     const int64_t mr = live ? m : m0;                   // a row past M reads and writes nothing (empty ranges)
     // the indices first (scalar loads), then the row's own loads, then the staging loads
@@ -375,7 +380,7 @@ __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
             a_hi[j] = __builtin_amdgcn_raw_buffer_load_b128(ar, c * 32u + 16u, 0, 2);
         }
     }
-    if (tid < NC) {                                     // wave-uniform (NC is a multiple of 64)
+    for (int t0 = tid; t0 < NC; t0 += THREADS) {         // wave-uniform (NC is a multiple of 64)
         auto put = [&](int t, v4u v, bool one_plus) {   // a bf16 chunk as two fp32 halves
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
@@ -386,27 +391,27 @@ __global__ void __launch_bounds__(512) rms_mod_quant_staged_kernel(RmsArgs a) {
                     const float x = u2f((e & 1) ? (w & 0xffff0000u) : (w << 16));
                     f[e] = one_plus ? 1.0f + x : x;
                 }
-                tabs[t][s][tid] = f;
+                tabs[t][s][t0] = f;
             }
         };
-        const v4u w = ld16(make_rsrc(a.weight, rb), tid);
-        const v4u sc = ld16(make_rsrc(a.scale + i0 * a.ld_scale, rb), tid);
-        const v4u sh = ld16(make_rsrc(a.shift + i0 * a.ld_shift, rb), tid);
+        const v4u w = ld16(make_rsrc(a.weight, rb), t0);
+        const v4u sc = ld16(make_rsrc(a.scale + i0 * a.ld_scale, rb), t0);
+        const v4u sh = ld16(make_rsrc(a.shift + i0 * a.ld_shift, rb), t0);
         v4u gt = {0, 0, 0, 0}, sbl = {0, 0, 0, 0}, sbh = {0, 0, 0, 0}, bs = {0, 0, 0, 0};
-        if (GATE) gt = ld16(make_rsrc(a.gate + i0 * a.ld_gate, rb), tid);
+        if (GATE) gt = ld16(make_rsrc(a.gate + i0 * a.ld_gate, rb), t0);
         if (B32) {
             const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sb, 2u * rb);
-            sbl = __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)tid * 32u, 0, 0);
-            sbh = __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)tid * 32u + 16u, 0, 0);
-            bs = ld16(make_rsrc(a.bias ? (const void*)a.bias : (const void*)a.weight, a.bias ? rb : 0u), tid);
+            sbl = __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)t0 * 32u, 0, 0);
+            sbh = __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)t0 * 32u + 16u, 0, 0);
+            bs = ld16(make_rsrc(a.bias ? (const void*)a.bias : (const void*)a.weight, a.bias ? rb : 0u), t0);
         }
         put(T_W, w, false);
         put(T_G, sc, true);
         put(T_B, sh, false);
         if (GATE) put(T_GATE, gt, false);
         if (B32) {
-            tabs[T_SB][0][tid] = __builtin_bit_cast(v4f, sbl);
-            tabs[T_SB][1][tid] = __builtin_bit_cast(v4f, sbh);
+            tabs[T_SB][0][t0] = __builtin_bit_cast(v4f, sbl);
+            tabs[T_SB][1][t0] = __builtin_bit_cast(v4f, sbh);
             put(T_BIAS, bs, false);
         }
     }
@@ -584,7 +589,8 @@ int launch_rms_cpl(const RmsArgs& a, hipStream_t st) {
 
 template <bool GATE, bool B32, int OUT, int CPL>
 int launch_rms_staged(const RmsArgs& a, hipStream_t st) {
-    const dim3 grid((unsigned)((a.M + 7) / 8)), block(512);
+    constexpr int rows = staged_rows<GATE>();
+    const dim3 grid((unsigned)((a.M + rows - 1) / rows)), block(64 * rows);
     if (a.H == 512 * CPL)
         hipLaunchKernelGGL((rms_mod_quant_staged_kernel<GATE, B32, OUT, CPL, true>), grid, block, 0, st, a);
     else
