@@ -322,14 +322,15 @@ __global__ void __launch_bounds__(256) rms_mod_quant_kernel(RmsArgs a) {
 
 // The producers and the out consumer with their tables staged in LDS as fp32: one wave per row, eight rows per
 // workgroup for the gated forms and four for the qkv producer (measured: with eight rows its index-run case took
-// 2 % and its random-index case 14 % longer, and the out consumer 14 % longer with four).  The modulation tables have one row per sample, so nearly every workgroup's rows share one index:
-// the workgroup converts once into fp32 LDS tables the weight row, 1 + scale and shift of its first row's index, and
-// for the gated forms gate of that index, for the fp32-branch form sb and the bias (the same fp32 values the
-// per-element arithmetic forms: bf16 -> fp32 is exact, 1 + scale the same fp32 add).  A wave whose row has that index
-// reads every table there at the point of use -- unpacks and an add fewer per element, and no table chunk held in
-// registers.  A wave whose row has another index (a sample boundary inside the workgroup, or an index outside the
-// tables) reads the index-dependent tables (gate, scale, shift) from global memory a few chunks at a time.  Arithmetic
-// and order otherwise as rms_mod_quant_row, so the outputs are bitwise the same.
+// 2 % and its random-index case 14 % longer, and the out consumer 14 % longer with four).  The modulation tables
+// have one row per sample, so nearly every workgroup's rows share one index: the workgroup converts once into fp32
+// LDS tables the weight row, 1 + scale and shift of its first row's index, and for the gated forms gate of that
+// index, for the fp32-branch form sb and the bias (the same fp32 values the per-element arithmetic forms: bf16 ->
+// fp32 is exact, 1 + scale the same fp32 add).  A wave whose row has that index reads every table there at the point
+// of use -- unpacks and an add fewer per element, and no table chunk held in registers.  A wave whose row has another
+// index (a sample boundary inside the workgroup, or an index outside the tables) reads the index-dependent tables
+// (gate, scale, shift) from global memory a few chunks at a time.  Arithmetic and order otherwise as
+// rms_mod_quant_row, so the outputs are bitwise the same.
 // LDS: table t, half s (elements 0-3 / 4-7 of a chunk), chunk c: tabs[t][s][c] (float4), so a wave's 16-byte reads
 // of one half are contiguous (no bank conflicts).  Tables: T_W weight, T_G 1 + scale, T_B shift, T_GATE gate,
 // T_SB sb, T_BIAS bias (zeros without one).
