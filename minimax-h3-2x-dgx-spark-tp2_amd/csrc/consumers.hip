@@ -25,6 +25,14 @@ namespace {
 
 using namespace h3;
 
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+// An output quad of bf16 pairs, stored non-temporally: the q / k / v rows stream through once (measured: the qkv
+// consumer 170.7 -> 165.0 us at 960x576).
+__device__ __forceinline__ void st_out8(uint16_t* p, uint32_t lo, uint32_t hi) {
+    __builtin_nontemporal_store((v2u){lo, hi}, reinterpret_cast<v2u*>(p));
+}
+
 struct QkArgs {
     const float* acc;           // fp32 [T, N], N >= (Hq + Hk) * 128: q heads, then k heads
     int64_t ld_acc;
@@ -200,7 +208,7 @@ __device__ __forceinline__ void qk_compute(const QkArgs& a, const QkIn& L, int l
     uint16_t* out = (isq ? a.out_q + t * a.ldq_t + (int64_t)h * a.ldq_h
                          : a.out_k + t * a.ldk_t + (int64_t)(h - a.Hq) * a.ldk_h) + 4 * k;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint2*>(out + 32 * i) = make_uint2(ob[2 * i], ob[2 * i + 1]);
+    for (int i = 0; i < 4; ++i) st_out8(out + 32 * i, ob[2 * i], ob[2 * i + 1]);
 }
 
 // A wave takes head group g of two consecutive tokens: both tokens' loads are issued before either is computed, and
@@ -244,7 +252,7 @@ __device__ __forceinline__ void v_pass(const QkArgs& a, int64_t t0, int64_t t1, 
                     x[e] = sam[u] * p;
                 }
             }
-            *reinterpret_cast<uint2*>(out + 32 * i) = make_uint2(cvt_bf16x2(x[0], x[1]), cvt_bf16x2(x[2], x[3]));
+            st_out8(out + 32 * i, cvt_bf16x2(x[0], x[1]), cvt_bf16x2(x[2], x[3]));
         }
     }
 }

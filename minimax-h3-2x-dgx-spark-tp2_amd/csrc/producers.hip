@@ -74,8 +74,10 @@ template <int AUX = 0>
 __device__ __forceinline__ v4u ld16(__amdgpu_buffer_rsrc_t r, int c) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)c * 16u, 0, AUX);
 }
+// Row stores are non-temporal: the rows stream through once (measured: the out consumer 178 -> 168 us, the qkv
+// producer's bf16 h form unchanged).
 __device__ __forceinline__ void st16(v4u v, __amdgpu_buffer_rsrc_t r, int c) {
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, (uint32_t)c * 16u, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (uint32_t)c * 16u, 0, 2);
 }
 
 // Wave-wide fp64 sum (xor butterfly; exact for the sums of squares of a bf16 row in all practical cases).
