@@ -321,7 +321,8 @@ __global__ void __launch_bounds__(256) scale_bias_cast_seg_kernel(const float* _
                 o[q] = OUT_DT ? fp16_rne(val) : bf16_rne(val);
             }
             const v2u ov = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
-            __builtin_amdgcn_raw_buffer_store_b64(ov, yr, (g0 + 256u * u) * 8u, 0, 0);
+            // non-temporal: the output streams through once (measured at 16 740 x 9216: 181.9 -> 165.8 us)
+            __builtin_amdgcn_raw_buffer_store_b64(ov, yr, (g0 + 256u * u) * 8u, 0, 2);
         }
     }
 }
