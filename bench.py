@@ -673,7 +673,14 @@ def main() -> None:
         qk_bytes = T * N * 4.0 + T * N * 2.0                         # product in, q / k / v bf16 out
         res["qkv_qk_norm_rope_16740x9216"] = {"ms": round(t_qk, 4), "GB/s": round(qk_bytes / (t_qk * 1e-3) / 1e9, 1),
                                               "frac_hbm": round(qk_bytes / (t_qk * 1e-3) / 1e9 / PEAK_GBS, 4)}
-        del x32, st
+        # the plain scale pass of the two-pass form on the same product (bf16 out): the consumer every other site of
+        # the two-pass level gets
+        y_sp = torch.empty((T, N), device=dev, dtype=torch.bfloat16)
+        t_sp = time_steps(lambda: ops.scale_bias_cast(x32, sa_t, sb_t, None, torch.bfloat16, out=y_sp), steps,
+                          warm) / steps
+        res["scale_pass_16740x9216"] = {"ms": round(t_sp, 4), "GB/s": round(qk_bytes / (t_sp * 1e-3) / 1e9, 1),
+                                        "frac_hbm": round(qk_bytes / (t_sp * 1e-3) / 1e9 / PEAK_GBS, 4)}
+        del x32, st, y_sp
         Mc, H = synthetic.CONFIGS["c3_ffn_1344x768_5s"]["M"], 3072
         x32 = torch.randn(Mc, H, device=dev, generator=gen) * 3000
         sa_c = torch.rand(Mc, device=dev, generator=gen) * 1e-3 + 1e-4
