@@ -14,7 +14,8 @@ against the 5.0 PFLOP/s FP8 dense MFMA peak.  Before the warm-up steps an explic
 ``--preroll-s`` seconds: the chip's clock moves over the first heavy calls, and the pre-roll makes the timed steps
 independent of how short the warm-up is.  The other measured workloads (the QKV projection at 960x576, the single
 linear, the FFN at 1344x768 5 s, the grouped launch, the reference's four H3 linears at its per-rank M = 42 848, the
-host cost of one dispatched call, the producers / consumers passes, the vendor GEMM, the socket power and clock of
+host cost of one dispatched call, the producers / consumers passes and the fc1 stash forms of the two-pass MLP (fp32
+gate/up product -> SwiGLU, and -> SwiGLU + requant), the vendor GEMM, the socket power and clock of
 each chain launch beside a register-only MFMA loop) are reported under ``workloads``.  ``cpu_baseline`` times the
 reference's torch CPU path (oracle/torch_path.py) of the same chain on a row sample, on this host's cores.  Synthetic
 seeded inputs, random-init weights (no checkpoints).
@@ -711,6 +712,23 @@ def main() -> None:
                                               "GB/s": round(fc2_bytes / (t_fc2 * 1e-3) / 1e9, 1),
                                               "frac_hbm": round(fc2_bytes / (t_fc2 * 1e-3) / 1e9 / PEAK_GBS, 4)}
         del x32, st, resid, ada, idx, idx_rand
+        # the fc1 stash forms of the two-pass MLP (1344x768 5 s, F = 8192): SwiGLU of the fp32 gate/up product to
+        # bf16 h (level 1), and SwiGLU + per-token requant to e4m3 q + scale (level 2)
+        F = 8192
+        x32 = torch.randn(Mc, 2 * F, device=dev, generator=gen) * 3000
+        sb_f = torch.rand(2 * F, device=dev, generator=gen) * 1e-3 + 1e-4
+        t_sw = time_steps(lambda: ops.scale_swiglu(x32, sa_c, sb_f), steps, warm) / steps
+        t_swq = time_steps(lambda: ops.scale_swiglu_quant(x32, sa_c, sb_f), steps, warm) / steps
+        sw_bytes = Mc * F * (8.0 + 2)                                # gate + up fp32 in; h bf16 out
+        swq_bytes = Mc * F * (8.0 + 1) + 4.0 * Mc                    # gate + up fp32 in; q + scale out
+        res["fc1_scale_swiglu_31248x2x8192"] = {"ms": round(t_sw, 4),
+                                                "GB/s": round(sw_bytes / (t_sw * 1e-3) / 1e9, 1),
+                                                "frac_hbm": round(sw_bytes / (t_sw * 1e-3) / 1e9 / PEAK_GBS, 4)}
+        res["fc1_scale_swiglu_quant_31248x2x8192"] = {"ms": round(t_swq, 4),
+                                                      "GB/s": round(swq_bytes / (t_swq * 1e-3) / 1e9, 1),
+                                                      "frac_hbm": round(swq_bytes / (t_swq * 1e-3) / 1e9 / PEAK_GBS,
+                                                                        4)}
+        del x32
         out["consumers_of_fp32_product"] = res
 
     # ---- CPU baseline: the reference's torch CPU path of the headline chain on a row sample ----

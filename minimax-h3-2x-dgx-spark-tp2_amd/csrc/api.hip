@@ -7,11 +7,12 @@
 
 #include "h3fp8_common.h"
 
-// The bf16 SiLU of every bf16 gate value, one table per device (128 KiB), filled once by h3fp8_init.
-__device__ uint16_t g_h3_silu_table[65536];
+// The bf16 SiLU of every bf16 gate value, one table per device (128 KiB), filled once by h3fp8_init.  Both tables
+// are 16-byte aligned: the kernels that copy them into LDS read 16 bytes per load.
+__device__ __attribute__((aligned(16))) uint16_t g_h3_silu_table[65536];
 
 // The compact rotated-key copy of the table (see h3fp8_common.h), filled from it by h3fp8_init.
-__device__ uint16_t g_h3_silu_rot[H3_SILU_ROT_LEN];
+__device__ __attribute__((aligned(16))) uint16_t g_h3_silu_rot[H3_SILU_ROT_LEN];
 
 // Counters of the e4m3 conversion self-check.
 __device__ unsigned long long g_h3_cvt_counts[4];

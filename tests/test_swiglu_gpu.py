@@ -59,6 +59,59 @@ def test_scale_swiglu_directed_values(cuda):
     _nan_aware_equal(bits16(h), O.scale_swiglu(x32.numpy(), sa.numpy(), sb.numpy()))
 
 
+def _swiglu_case(M: int, F: int, pad: int, bias: bool, seed: int):
+    """An fp32 product [M, 2F] (rows padded by pad floats) with values that force the full-table lookups: a zero
+    gate (row 1), a -0 up (row 2), a NaN gate (row 3, a NaN row maximum) and an inf up (row 4)."""
+    g = torch.Generator().manual_seed(seed)
+    base = torch.randn(M, 2 * F + pad, generator=g) * 3000
+    base[1, 3] = 0.0
+    base[2, F + 5] = -0.0
+    base[3, 7] = float("nan")
+    base[4, F + 1] = float("inf")
+    sa = torch.rand(M, generator=g) * 0.01 + 0.001
+    sb = torch.rand(2 * F, generator=g) * 0.01 + 0.001
+    bb = (torch.randn(2 * F, generator=g) * 0.1).to(torch.bfloat16) if bias else None
+    return base, sa, sb, bb
+
+
+# The LDS-table kernels of the fp32 passes, one case per launch shape: 1, 2 and 4 column groups per thread over 4, 8
+# and 16 waves (F = 128 ... 16 384) and F past that (the one-workgroup-per-row kernel); several rows per workgroup
+# (M = 5001), odd M (a row pair with one row), padded rows.
+@pytest.mark.parametrize("M,F,pad", [(5001, 128, 0), (2501, 1000, 8), (700, 2048, 0), (300, 4000, 0), (101, 8184, 4),
+                                     (40, 12000, 0), (23, 16384, 0), (9, 16388, 0)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_scale_swiglu_lds_forms(cuda, M, F, pad, bias):
+    from h3_tp2_amd import ops
+    base, sa, sb, bb = _swiglu_case(M, F, pad, bias, seed=M * 3 + F)
+    xd = base.to(cuda)[:, :2 * F]
+    bd = bb.to(cuda) if bias else None
+    h = ops.scale_swiglu(xd, sa.to(cuda), sb.to(cuda), bd)
+    q, s = ops.scale_swiglu_quant(xd, sa.to(cuda), sb.to(cuda), bd)
+    torch.cuda.synchronize()
+    x = base[:, :2 * F].contiguous().numpy()
+    bbits = bits16(bb) if bias else None
+    _nan_aware_equal(bits16(h), O.scale_swiglu(x, sa.numpy(), sb.numpy(), bbits))
+    assert_quant_equal(q, s, *O.scale_swiglu_quant(x, sa.numpy(), sb.numpy(), bbits))
+
+
+# Column scales that are not one contiguous vector take the element-wise and one-workgroup-per-row kernels.
+@pytest.mark.parametrize("sb_kind", ["strided", "scalar"])
+def test_scale_swiglu_noncontiguous_scales(cuda, sb_kind):
+    from h3_tp2_amd import ops
+    M, F = 37, 2000
+    base, sa, sb, bb = _swiglu_case(M, F, 0, True, seed=5)
+    if sb_kind == "strided":
+        sbd = torch.stack([sb, sb * 2], dim=1).reshape(-1).to(cuda)[::2]      # stride 2
+    else:
+        sb = torch.full((2 * F,), 0.004)
+        sbd = torch.tensor([0.004]).to(cuda)
+    h = ops.scale_swiglu(base.to(cuda), sa.to(cuda), sbd, bb.to(cuda))
+    q, s = ops.scale_swiglu_quant(base.to(cuda), sa.to(cuda), sbd, bb.to(cuda))
+    torch.cuda.synchronize()
+    _nan_aware_equal(bits16(h), O.scale_swiglu(base.numpy(), sa.numpy(), sb.numpy(), bits16(bb)))
+    assert_quant_equal(q, s, *O.scale_swiglu_quant(base.numpy(), sa.numpy(), sb.numpy(), bits16(bb)))
+
+
 @pytest.mark.parametrize("M,F", [(1, 14336), (200, 14336), (64, 8192), (5, 40000)])
 def test_silu_mul_quant(cuda, M, F):
     from h3_tp2_amd import ops
