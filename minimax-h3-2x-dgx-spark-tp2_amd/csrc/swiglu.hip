@@ -239,6 +239,80 @@ __global__ void __launch_bounds__(64 * SMQ_WAVES) silu_mul_quant_lds_kernel(cons
     }
 }
 
+// The same pass for rows too wide for one wave (8192 < F <= 16 384): 16 waves per row, thread t owns the 16-byte
+// chunks t + 1024 j (j < CPL) of the gate and of the up half; the row maximum is a wave shuffle plus an LDS exchange
+// behind a bare s_barrier, and the next row's loads are issued before it, so they stay in flight across it and the
+// stores.  One workgroup per CU (the 128 KiB table).
+constexpr int SMQW_WAVES = 16;
+template <int CPL>
+__global__ void __launch_bounds__(64 * SMQW_WAVES) silu_mul_quant_wide_kernel(const uint16_t* __restrict__ x,
+                                                                             int64_t ldx, int64_t M, int64_t F,
+                                                                             const uint16_t* __restrict__ silu,
+                                                                             uint8_t* __restrict__ q, int64_t ldq,
+                                                                             float* __restrict__ scale) {
+    constexpr int THREADS = 64 * SMQW_WAVES;
+    __shared__ __attribute__((aligned(16))) uint16_t tab[65536];
+    __shared__ uint32_t red[2][SMQW_WAVES];
+    for (int i = threadIdx.x; i < 65536 / 8; i += THREADS)
+        reinterpret_cast<v4u*>(tab)[i] = reinterpret_cast<const v4u*>(silu)[i];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float pz = 0.0f;
+    asm volatile("" : "+v"(pz));                        // an opaque +0 (the add below must not be folded away)
+    v4u gv[CPL], uv[CPL];
+    auto load_row = [&](int64_t m) {
+        // loads past F read zeros: gate 0 looks up silu(0) = 0, so those columns give h = +0
+        const __amdgpu_buffer_rsrc_t gr = make_rsrc(x + m * ldx, (uint32_t)(2 * F));
+        const __amdgpu_buffer_rsrc_t ur = make_rsrc(x + m * ldx + F, (uint32_t)(2 * F));
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t off = (threadIdx.x + THREADS * (uint32_t)j) * 16u;
+            gv[j] = __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 2);
+            uv[j] = __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, 2);
+        }
+    };
+    int64_t m = blockIdx.x;
+    if (m < M) load_row(m);
+    __syncthreads();
+    for (int par = 0; m < M; m += gridDim.x, par ^= 1) {
+        uint32_t h[CPL][4];
+        u16x2_t mx2 = {0, 0};
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t g2 = gv[j][k], u2 = uv[j][k];
+                const float u0 = bf16_to_f32(u2 & 0xffffu) + pz, u1 = u2f(u2 & 0xffff0000u) + pz;   // -0 up -> +0
+                const float s0 = bf16_to_f32(tab[g2 & 0xffffu]), s1 = bf16_to_f32(tab[g2 >> 16]);
+                h[j][k] = cvt_bf16x2(s0 * u0, s1 * u1);
+                mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2_t, h[j][k] & 0x7fff7fffu));
+            }
+        if (m + gridDim.x < M) load_row(m + gridDim.x);
+        uint32_t mx = mx2[0] > mx2[1] ? (uint32_t)mx2[0] : (uint32_t)mx2[1];
+        mx = wave_max_u32(mx << 16);
+        if (lane == 0) red[par][wave] = mx;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // no fence: the row loads stay in flight
+#pragma unroll
+        for (int w = 0; w < SMQW_WAVES; ++w) mx = mx > red[par][w] ? mx : red[par][w];
+        const float s = row_scale(u2f(mx));
+        const float inv = inv_scale(s);
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + m * ldq, (uint32_t)F);
+        if (mx < 0x7f800000u) {                          // workgroup-uniform: finite row maximum
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const v2u v = {quant_pairs<true>(h[j][0], h[j][1], inv), quant_pairs<true>(h[j][2], h[j][3], inv)};
+                __builtin_amdgcn_raw_buffer_store_b64(v, qr, (threadIdx.x + THREADS * (uint32_t)j) * 8u, 0, 2);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const v2u v = {quant_pairs<false>(h[j][0], h[j][1], inv), quant_pairs<false>(h[j][2], h[j][3], inv)};
+                __builtin_amdgcn_raw_buffer_store_b64(v, qr, (threadIdx.x + THREADS * (uint32_t)j) * 8u, 0, 2);
+            }
+        }
+        if (threadIdx.x == 0) scale[m] = s;
+    }
+}
+
 // fp32 product -> bf16 h, elementwise: one thread per group of 4 columns.
 __global__ void __launch_bounds__(256) scale_swiglu_kernel(const float* __restrict__ x, int64_t ldx, int64_t M,
                                                            int64_t F, EpiArgs e, const uint16_t* __restrict__ silu,
@@ -574,17 +648,24 @@ void launch_scale_bias_cast_seg(const float* x, int64_t ldx, int64_t M, int64_t 
     else hipLaunchKernelGGL((scale_bias_cast_seg_kernel<OUT_DT, 4>), grid, block, 0, st, x, ldx, N, e, y, ldy, M);
 }
 
-// The persistent LDS-table form of the bf16-source pass, when its 16-byte loads and 8-byte stores are aligned and a row
-// fits in registers (F <= 8192); returns false to take the one-workgroup-per-row kernel instead.
+// The persistent LDS-table forms of the bf16-source pass, when their 16-byte loads and 8-byte stores are aligned: one
+// wave per row for F <= 8192, 16 waves per row for F <= 16 384; returns false to take the one-workgroup-per-row kernel.
 bool launch_silu_mul_quant_lds(const void* x, int64_t ldx, int64_t M, int64_t F, const uint16_t* silu, void* q,
                                int64_t ldq, float* scale, hipStream_t st) {
     const int64_t cpl = ((F >> 3) + 63) / 64;
-    if (F % 8 != 0 || ldx % 8 != 0 || ldq % 8 != 0 || ((uintptr_t)q & 7) != 0 || cpl > 16) return false;
+    if (F % 8 != 0 || ldx % 8 != 0 || ldq % 8 != 0 || ((uintptr_t)q & 7) != 0 || F > 2 * 8 * 64 * SMQW_WAVES)
+        return false;
     // buffer descriptors need 4-byte aligned bases: every row start is (16-byte x, 8-byte q, even strides)
-    const int64_t wgs = std::min<int64_t>((M + SMQ_WAVES - 1) / SMQ_WAVES, h3host::cu_count());
-    dim3 grid((unsigned)std::max<int64_t>(1, wgs)), block(64 * SMQ_WAVES);
     const uint16_t* xp = (const uint16_t*)x;
     uint8_t* qp = (uint8_t*)q;
+    if (cpl > 16) {                                      // 8192 < F <= 16 384: 16 waves per row, 2 chunks per lane
+        const int64_t wgs = std::min<int64_t>(M, h3host::cu_count());
+        hipLaunchKernelGGL((silu_mul_quant_wide_kernel<2>), dim3((unsigned)wgs), dim3(64 * SMQW_WAVES), 0, st, xp, ldx,
+                           M, F, silu, qp, ldq, scale);
+        return true;
+    }
+    const int64_t wgs = std::min<int64_t>((M + SMQ_WAVES - 1) / SMQ_WAVES, h3host::cu_count());
+    dim3 grid((unsigned)std::max<int64_t>(1, wgs)), block(64 * SMQ_WAVES);
 #define H3_L(N) hipLaunchKernelGGL((silu_mul_quant_lds_kernel<N>), grid, block, 0, st, xp, ldx, M, F, silu, qp, ldq, scale)
     if (cpl <= 1) H3_L(1);
     else if (cpl <= 2) H3_L(2);

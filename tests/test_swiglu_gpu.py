@@ -125,10 +125,12 @@ def test_silu_mul_quant(cuda, M, F):
     assert_quant_equal(q, s, *O.quant_rows(hh))
 
 
-# Shapes of the persistent LDS-table form (F <= 8192, F % 8 == 0): ragged 16-byte chunk counts per lane (F = 1000,
-# 520, 8184), one workgroup with idle waves (M = 3), several rows per wave (M = 4500 over at most 2048 waves), and a
-# strided input (a row stride past 2F).
-@pytest.mark.parametrize("M,F,pad", [(3, 1000, 0), (4500, 520, 0), (2600, 8192, 0), (77, 8184, 0), (300, 4096, 24)])
+# Shapes of the persistent LDS-table forms (F % 8 == 0; one wave per row up to F = 8192, 16 waves per row up to
+# 16 384): ragged 16-byte chunk counts per lane (F = 1000, 520, 8184, 9000, 12 008), one workgroup with idle waves
+# (M = 3), several rows per wave or workgroup (M = 4500 over at most 2048 waves, M = 2100 over 256 workgroups), and
+# strided inputs (a row stride past 2F).
+@pytest.mark.parametrize("M,F,pad", [(3, 1000, 0), (4500, 520, 0), (2600, 8192, 0), (77, 8184, 0), (300, 4096, 24),
+                                     (2100, 9000, 0), (37, 16384, 8), (3, 12008, 0)])
 def test_silu_mul_quant_persistent_form(cuda, M, F, pad):
     from h3_tp2_amd import ops
     g = torch.Generator().manual_seed(M * 7 + F)
