@@ -112,6 +112,36 @@ def test_scale_swiglu_noncontiguous_scales(cuda, sb_kind):
     assert_quant_equal(q, s, *O.scale_swiglu_quant(base.numpy(), sa.numpy(), sb.numpy(), bits16(bb)))
 
 
+def test_swiglu_passes_captured_in_a_graph_replay_bitwise(cuda):
+    """The fp32 SwiGLU passes (the LDS-table kernels, with a bias) and the 16-wave bf16 pass captured in one HIP graph
+    (torch.cuda.graph) after an eager call: three replays, each after every output was overwritten and the same work
+    ran eagerly, with a synchronisation in between, equal the eager results byte for byte."""
+    from h3_tp2_amd import ops
+    base, sa, sb, bb = _swiglu_case(300, 4000, 0, True, seed=21)
+    x, sa_d, sb_d, bb_d = base.to(cuda), sa.to(cuda), sb.to(cuda), bb.to(cuda)
+    xb = (torch.randn(40, 2 * 12008, generator=torch.Generator().manual_seed(22)) * 4).to(torch.bfloat16).to(cuda)
+
+    def run():
+        return (ops.scale_swiglu(x, sa_d, sb_d, bb_d), *ops.scale_swiglu_quant(x, sa_d, sb_d, bb_d),
+                *ops.silu_mul_quant(xb))
+
+    ref = [t.clone() for t in run()]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = run()
+    for rep in range(3):
+        for t in outs:
+            t.view(torch.uint8).fill_(0x7F)
+        run()                                               # eager work between the replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for t, r in zip(outs, ref):
+            assert torch.equal(t.view(torch.uint8), r.view(torch.uint8)), f"replay {rep}"
+    del g
+
+
 @pytest.mark.parametrize("M,F", [(1, 14336), (200, 14336), (64, 8192), (5, 40000)])
 def test_silu_mul_quant(cuda, M, F):
     from h3_tp2_amd import ops
