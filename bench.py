@@ -681,7 +681,19 @@ def main() -> None:
                           warm) / steps
         res["scale_pass_16740x9216"] = {"ms": round(t_sp, 4), "GB/s": round(qk_bytes / (t_sp * 1e-3) / 1e9, 1),
                                         "frac_hbm": round(qk_bytes / (t_sp * 1e-3) / 1e9 / PEAK_GBS, 4)}
-        del x32, st, y_sp
+        # the GEMM of the two-pass form: kernel 2 writing the raw fp32 product that the consumers above read (here
+        # into the same buffer), QKV 3072 -> 9216 at 960x576 5 s
+        qa, s_qa = ops.quant_rows(synthetic.activations(T, 3072, seed=11, n_out=3).to(dev))
+        wq, s_wq = quantised_weight(N, 3072, seed=12)
+        t_g32 = time_steps(lambda: ops.gemm(qa, wq, s_qa, s_wq, torch.float32, out=x32), steps, warm) / steps
+        g32_flops = 2.0 * T * N * 3072
+        res["two_pass_qkv_gemm_fp32_16740x9216x3072"] = {
+            "ms": round(t_g32, 4), "TFLOP/s": round(tflops(g32_flops, t_g32), 1),
+            "frac_mfma": round(tflops(g32_flops, t_g32) / PEAK_TFLOPS, 4),
+            "with_qk_consumer_ms": round(t_g32 + t_qk, 4),
+            "note": "kernel 2 storing the fp32 accumulator (2x the bf16 output bytes); with the fused qk consumer this is "
+                    "the two-pass form of the QKV site"}
+        del x32, st, y_sp, qa, wq
         Mc, H = synthetic.CONFIGS["c3_ffn_1344x768_5s"]["M"], 3072
         x32 = torch.randn(Mc, H, device=dev, generator=gen) * 3000
         sa_c = torch.rand(Mc, device=dev, generator=gen) * 1e-3 + 1e-4

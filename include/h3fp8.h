@@ -35,8 +35,9 @@ extern "C" {
 
 #define H3FP8_DT_BF16 0
 #define H3FP8_DT_FP16 1
-#define H3FP8_DT_F32 2       /* h3fp8_gemm only: the raw fp32 accumulator, scales ignored (probe mode, as the
-                                reference's fused kernel with OUT 0, h3_tp2/fp8_gemm.py:74, :98-99) */
+#define H3FP8_DT_F32 2       /* h3fp8_gemm only: the raw fp32 accumulator, scales ignored (the reference's fused
+                                kernel with OUT 0, h3_tp2/fp8_gemm.py:74, :98-99; here also the product of the
+                                two-pass form, whose scale pass or fused consumer follows) */
 
 /* ABI version (H3FP8_ABI_VERSION of the build) and the last error of the calling thread. */
 int h3fp8_abi_version(void);

@@ -541,26 +541,41 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
     const int mrow0 = tm * BM + wm * 128;               // first token row of the wave
     const float* sa_l = reinterpret_cast<const float*>(lds + Lds<EPI>::SCALES_OFF + set * SCALE_SET);
     const float* sb_l = sa_l + 256;
+    uint8_t* stg = lds + Lds<EPI>::STAGING_OFF + wave * Lds<EPI>::STAGING_PER_WAVE;
     if (OUT_DT == H3FP8_DT_F32) {
-        // probe mode: the raw fp32 accumulators, scales / bias / rounding not applied (16-byte stores per lane)
-        float* yf = reinterpret_cast<float*>(p.y);
+        // the raw fp32 accumulators (scales / bias / rounding not applied), staged one 32 x 32 MFMA block at a time:
+        // lane l writes the 4 x 4 channels of token l & 31 as 16-byte chunks (8q + 4 hi) / 4 of that token's 128-byte
+        // row, chunk c stored at c ^ (row % 8); the wave then reads back 8 rows of 128 bytes per instruction and every
+        // store writes whole 128-byte row segments (rows past M are out of the descriptor's range, columns past N get
+        // an out-of-range offset)
+        const __amdgpu_buffer_rsrc_t yr = make_rsrc(p.y, p.y_bytes);
+        const uint32_t row4 = (uint32_t)p.ldy * 4u;
+        const int c = lane & 7;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int j = 0; j < 4; ++j) {
+                wave_sync();                            // the previous block's reads before these writes
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int n = wcol + 32 * i + 8 * q + 4 * hi;
-                    const int m = mrow0 + 32 * j + mj;
-                    if (n < p.N && m < p.M) {
-                        const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                       acc[i][j][4 * q + 3]};
-                        *reinterpret_cast<v4f*>(yf + (int64_t)m * p.ldy + n) = v;
-                    }
+                for (int q = 0; q < 4; ++q) {
+                    const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    *reinterpret_cast<v4f*>(stg + mj * 128 + (((2 * q + hi) ^ (mj & 7)) << 4)) = v;
                 }
+                wave_sync();                            // every lane's writes before any lane's reads
+                v4u v[4];
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const int ml = it * 8 + (lane >> 3);
+                    v[it] = *reinterpret_cast<const v4u*>(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+                }
+                const int n = wcol + 32 * i + 4 * c;
+                const uint32_t off = (n < p.N) ? (uint32_t)(mrow0 + 32 * j + (lane >> 3)) * row4 + (uint32_t)n * 4u : OOB;
+#pragma unroll
+                for (int it = 0; it < 4; ++it)
+                    __builtin_amdgcn_raw_buffer_store_b128(v[it], yr, off + (uint32_t)it * 8u * row4, 0, 0);
+            }
         return;
     }
-    uint8_t* stg = lds + Lds<EPI>::STAGING_OFF + wave * Lds<EPI>::STAGING_PER_WAVE;
     // element (ml, cl) of the 32 x 64 staging tile: row ml, 16-byte chunk (cl / 8) ^ (ml % 8), 8-byte half (cl / 4) % 2
     auto put4 = [&](int ml, int cl, uint32_t lo, uint32_t h2) {
         const int ch = (cl >> 3) ^ (ml & 7);
@@ -843,9 +858,8 @@ __global__ void __launch_bounds__(256, 1) gemm_kernel(GroupedParams gp) {
 
         v16f acc[4][4];
         int ks = 0;
-        if (OUT_DT != H3FP8_DT_F32 && nk > 1) {
-            // the first k-step's MFMAs start every accumulator block from 0 (the raw-accumulator probe, a test form,
-            // clears instead: it keeps its registers clear of scratch that way)
+        if (nk > 1) {
+            // the first k-step's MFMAs start every accumulator block from 0 (C = the constant 0)
             kstep<EPI, true, true>(lds, lds0, g, I, wofs, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
             if (I.valid) cursor_next<EPI, GROUPED>(I, gp, lds0, wave, lane);
             ++g;
@@ -1678,7 +1692,7 @@ GemmParams make_params(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t 
     p.w_rows = (int)w_rows;
     p.a_bytes = (uint32_t)((M - 1) * lda + K);
     p.w_bytes = (uint32_t)((w_rows - 1) * ldw + K);
-    p.y_bytes = (uint32_t)(((M - 1) * ldy + N) * 2);   // bf16 / fp16 (the fp32 probe stores without the descriptor)
+    p.y_bytes = (uint32_t)(((M - 1) * ldy + N) * 2);   // bf16 / fp16 (run_gemm resets it for fp32 outputs)
     const int64_t n_tile_cols = swiglu ? (BN / 2) : BN;
     p.tiles_m = (int)((M + BM - 1) / BM);
     p.tiles_n = (int)((N + n_tile_cols - 1) / n_tile_cols);
@@ -1712,6 +1726,7 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
                               row_amax ? row_amax + r0 : nullptr, silu, epi == EPI_SWIGLU);
         gp.n = 1;
         if (epi == EPI_SWIGLU) gp.g[0].silu_rot = h3host::silu_rot_ptr();
+        if (out_dt == H3FP8_DT_F32) gp.g[0].y_bytes = (uint32_t)(((Mi - 1) * ldy + N) * 4);
         const int rc = launch_split(gp, epi, out_dt, bias != nullptr, st);
         if (rc) return rc;
     }
@@ -1761,7 +1776,7 @@ int h3fp8_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const flo
     H3_REQUIRE(out_dtype == H3FP8_DT_BF16 || out_dtype == H3FP8_DT_FP16 || out_dtype == H3FP8_DT_F32,
                "h3fp8_gemm: bad out_dtype %d", out_dtype);
     H3_REQUIRE(out_dtype != H3FP8_DT_F32 || (!bias && !row_amax && ldy % 4 == 0),
-               "h3fp8_gemm: the fp32 accumulator probe takes no bias or row_amax and needs ldy %% 4 == 0");
+               "h3fp8_gemm: the raw fp32 accumulator output takes no bias or row_amax and needs ldy %% 4 == 0");
     if (M == 0 || N == 0) return H3FP8_OK;
     rc = h3host::ensure_device_init();
     if (rc) return rc;

@@ -180,11 +180,12 @@ def gemm(a: torch.Tensor, w: torch.Tensor, scale_a: torch.Tensor, scale_b: torch
          row_amax: torch.Tensor | None = None) -> torch.Tensor:
     """y [M, N] = round(sa[m] * (sb[n] * (a @ w.T)[m, n])) (+ bias by one fma); ``w`` is the [N, K] weight.
     With ``row_amax`` ([M] fp32) the epilogue also reduces max |y| per row (for the next layer's quant).
-    ``out_dtype=torch.float32`` returns the raw fp32 accumulator (probe mode: scales ignored)."""
+    ``out_dtype=torch.float32`` returns the raw fp32 accumulator (scales ignored: the two-pass form's product, whose
+    scale pass or fused consumer follows; the reference's OUT 0)."""
     N = w.shape[0]
     M, sa, sa_st, sb, sb_st = _gemm_args(a, w, scale_a, scale_b, N)
     if out_dtype not in _DT:
-        raise ValueError(f"out_dtype must be bf16, fp16 or fp32 (probe), got {out_dtype}")
+        raise ValueError(f"out_dtype must be bf16, fp16 or fp32 (the raw accumulator), got {out_dtype}")
     if bias is not None and (bias.dim() != 1 or bias.numel() != N or bias.dtype != out_dtype
                              or bias.device != a.device or not bias.is_contiguous()):
         raise ValueError("bias must be a contiguous [N] vector in the output dtype on the operands' device")
