@@ -1226,14 +1226,22 @@ __device__ __forceinline__ void h3s_kstep(uint8_t* lds, uint32_t lds0, int s0, c
     }
 }
 
-// Epilogue of a wave's NI x NJ MFMA blocks straight from the accumulators (no LDS staging): register 4q + r of block
-// (i, j) is channel col0 + 32 i + 8 q + 4 (lane >> 5) + r of token mrow0 + 32 j + (lane & 31); sa_l[sa0 + t] and
-// sb_l[sb0 + c] (LDS) hold the scales of token mrow0 + t and channel col0 + c.  Each lane stores its 4 consecutive channels (8 bytes, 16
-// contiguous bytes with the partner lane l ^ 32).  Rows past M fall outside the output descriptor's range, columns past
-// N get an out-of-range offset.
-template <int OUT_DT, bool HAS_BIAS, int EPI, int NI, int NJ, int AI, int AJ>
+// Epilogue of a wave's NI x NJ MFMA blocks from the accumulators: register 4q + r of block (i, j) is channel
+// col0 + 32 i + 8 q + 4 (lane >> 5) + r of token mrow0 + 32 j + (lane & 31); sa_l[sa0 + t] and sb_l[sb0 + c] (LDS)
+// hold the scales of token mrow0 + t and channel col0 + c.  Without staging each lane stores its 4 consecutive
+// channels (8 bytes, 16 contiguous bytes with the partner lane l ^ 32), so a store instruction touches 32 rows.
+// STAGED (bf16 / fp16 outputs): the 32 tokens of block row j go through the wave's LDS area `stg` (rows of NI x 64
+// bytes at a stride padded by 16 bytes) and come back as 16-byte chunks, chunk c of row t at lane (32 t + c) % 64 of
+// instruction (32 t + c) / 64 -- every store then writes whole row segments of NI x 64 bytes (the store path handles
+// about one 128-byte line per cycle, so the lines an instruction touches are what it costs).  Rows past M fall
+// outside the output descriptor's range, columns past N get an out-of-range offset.
+template <int OUT_DT, bool HAS_BIAS, int EPI, int NI, int NJ, int AI, int AJ, bool STAGED = false>
 __device__ __forceinline__ void reg_epilogue(const GemmParams& p, int col0, int mrow0, const float* sa_l, int sa0,
-                                             const float* sb_l, int sb0, int lane, v16f (&acc)[AI][AJ]) {
+                                             const float* sb_l, int sb0, int lane, v16f (&acc)[AI][AJ],
+                                             uint8_t* stg = nullptr) {
+    constexpr int CH = NI * 4;                          // 16-byte chunks per staged token row
+    constexpr int RS = CH * 16 + 16;                    // staged row stride (padded: rows fall on other banks)
+    static_assert(!STAGED || (32 * CH) % 64 == 0, "whole store instructions per block row");
     static_assert(NI <= AI && NJ <= AJ, "blocks of the accumulator array");
     const int hi = lane >> 5, mj = lane & 31;
     if (OUT_DT == H3FP8_DT_F32) {
@@ -1261,6 +1269,7 @@ __device__ __forceinline__ void reg_epilogue(const GemmParams& p, int col0, int 
         const int m = mrow0 + 32 * j + mj;
         const float sam = sa_l[sa0 + 32 * j + mj];
         uint32_t rmax = 0;
+        if (STAGED) wave_sync();                        // the previous block row's reads before these writes
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -1290,10 +1299,29 @@ __device__ __forceinline__ void reg_epilogue(const GemmParams& p, int col0, int 
                 if (EPI == EPI_AMAX && n < p.N && m < p.M)
                     rmax = OUT_DT ? max_abs_f16x2(max_abs_f16x2(rmax, lo), hi2)
                                   : max_abs_bf16x2(max_abs_bf16x2(rmax, lo), hi2);
-                const uint32_t off = (n < p.N) ? (uint32_t)m * row2 + (uint32_t)n * 2u : OOB;
                 const v2u32 val = {lo, hi2};
-                __builtin_amdgcn_raw_buffer_store_b64(val, yr, off, 0, 0);
+                if (STAGED) {
+                    *reinterpret_cast<v2u32*>(stg + mj * RS + (4 * i + q) * 16 + 8 * hi) = val;
+                } else {
+                    const uint32_t off = (n < p.N) ? (uint32_t)m * row2 + (uint32_t)n * 2u : OOB;
+                    __builtin_amdgcn_raw_buffer_store_b64(val, yr, off, 0, 0);
+                }
             }
+        if (STAGED) {
+            wave_sync();                                // every lane's writes before any lane's reads
+            constexpr int NS = 32 * CH / 64;
+            v4u v[NS];
+            uint32_t off[NS];
+#pragma unroll
+            for (int s2 = 0; s2 < NS; ++s2) {           // all reads before the first store
+                const int idx = 64 * s2 + lane, t = idx / CH, c = idx - t * CH;
+                v[s2] = *reinterpret_cast<const v4u*>(stg + t * RS + c * 16);
+                const int n = col0 + 8 * c;
+                off[s2] = (n < p.N) ? (uint32_t)(mrow0 + 32 * j + t) * row2 + (uint32_t)n * 2u : OOB;
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < NS; ++s2) __builtin_amdgcn_raw_buffer_store_b128(v[s2], yr, off[s2], 0, 0);
+        }
         if (EPI == EPI_AMAX) {
             const uint32_t o = (uint32_t)__shfl_xor((int)rmax, 32, 64);
             rmax = rmax > o ? rmax : o;
@@ -1379,7 +1407,9 @@ constexpr int W192_A = W192_WR * ROWB;                  // token rows start afte
 constexpr int W192_NSTAGE = 3;
 constexpr int W192_SCALES_OFF = W192_NSTAGE * W192_STAGE;
 constexpr int W192_JUNK_OFF = W192_SCALES_OFF + SCALE_SET;
-constexpr int W192_LDS = W192_JUNK_OFF + 512;
+constexpr int W192_STG_OFF = W192_JUNK_OFF + 512;      // the epilogue's staging: per wave 32 rows of 192 + 16 bytes
+constexpr int W192_STG_PER_WAVE = 32 * (3 * 64 + 16);
+constexpr int W192_LDS = W192_STG_OFF + 4 * W192_STG_PER_WAVE;
 static_assert(W192_LDS <= 160 * 1024, "LDS of one CU");
 constexpr int W192_LOADS = 12;                          // per wave and k-step: 6 weight + 4 token + 2 scale loads
 constexpr int W192_GROUP_M = 8;                         // token-tile rows per group of the XCD-contiguous tile map
@@ -1543,8 +1573,9 @@ __global__ void __launch_bounds__(256, 1) gemm_w192_kernel(GemmParams p) {
     }
     w192_kstep<false>(lds, lds0, s0, L.nk - 1, L, wave, wn, wm, lane, acc, fa0, fb0, fa1, fb1);
     const float* sa_l = reinterpret_cast<const float*>(lds + W192_SCALES_OFF);
-    reg_epilogue<OUT_DT, HAS_BIAS, EPI, 3, 2>(p, tn * W192_WR + wn * 96, tm * W192_TR + wm * 64, sa_l, wm * 64,
-                                              sa_l + 256, wn * 96, lane, acc);
+    reg_epilogue<OUT_DT, HAS_BIAS, EPI, 3, 2, 3, 2, true>(p, tn * W192_WR + wn * 96, tm * W192_TR + wm * 64, sa_l,
+                                                          wm * 64, sa_l + 256, wn * 96, lane, acc,
+                                                          lds + W192_STG_OFF + wave * W192_STG_PER_WAVE);
     wait_vm0();                                         // the trailing zero-fill loads have landed before the exit
 }
 
