@@ -158,6 +158,14 @@ __device__ __forceinline__ void dma16(v4u desc, uint32_t lds_base, uint32_t voff
                  : "memory", "m0");
 }
 
+// The same load with the non-temporal hint, for operands that stream through once.
+__device__ __forceinline__ void dma16_nt(v4u desc, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(desc)
+                 : "memory", "m0");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
     typedef const __attribute__((address_space(3))) uint8_t* lds_u8;
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8)(p));
@@ -918,7 +926,8 @@ struct RowsRing {
     static_assert(DEPTH >= 2 && LOADS * (DEPTH - 1) <= 63, "vmcnt range");
 };
 
-template <int OUT_DT, bool HAS_BIAS, bool AMAX, int MB>
+// NT: the weight loads carry the non-temporal hint (chosen by the launcher, see launch_rows_t).
+template <int OUT_DT, bool HAS_BIAS, bool AMAX, int MB, bool NT>
 __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
     constexpr int ROWS_DEPTH = RowsRing<MB>::DEPTH;
     constexpr int ROWS_STAGE = RowsRing<MB>::STAGE;
@@ -950,7 +959,11 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
         for (int i = 0; i < 4; ++i) {
             const uint32_t c = (uint32_t)ks * BK + 16u * lch[i & 1];
             const bool in = c < (uint32_t)p.K;
-            if (i < ROWS_RW / 8) dma16(dw, st + (uint32_t)i * 8 * ROWB, in && wrow[i] != OOB ? wrow[i] + c : OOB);
+            if (i < ROWS_RW / 8) {
+                const uint32_t off = in && wrow[i] != OOB ? wrow[i] + c : OOB;
+                if (NT) dma16_nt(dw, st + (uint32_t)i * 8 * ROWB, off);
+                else dma16(dw, st + (uint32_t)i * 8 * ROWB, off);
+            }
             if (i < MB)
                 dma16(da, st + ROWS_RW * ROWB + (uint32_t)i * 8 * ROWB, in && arow[i] != OOB ? arow[i] + c : OOB);
         }
@@ -1036,11 +1049,24 @@ __global__ void __launch_bounds__(64) gemm_rows_kernel(GemmParams p) {
     }
 }
 
+// With at least 4 waves per CU of the one-token-group form the weight stream is bandwidth-bound and its loads take the
+// non-temporal hint; with fewer waves (each streaming more k-steps) or the four-group form the hint made it slower.
+// Measured (one process, interleaved, median of 7, outputs identical), M x N x K: 2 x 18 432 x 3072 (1152 waves)
+// 10.6 -> 9.2 us, 2 x 36 864 x 3072 19.1 -> 17.6, 5 x 18 432 x 3072 10.5 -> 9.3; but 2 x 9216 x 3072 (576 waves)
+// 5.8 -> 6.2, 2 x 12 288 x 3072 6.7 -> 6.9, 32 x 18 432 x 3072 (four groups) 12.1 -> 14.2, 32 x 3072 x 8192
+// 11.9 -> 15.3; 2 x 16 384 x 8192 (1024 waves of 64 k-steps) 23.0 either way.
 template <int OUT_DT, bool HAS_BIAS, bool AMAX>
 int launch_rows_t(const GemmParams& p, hipStream_t st) {
-    const dim3 grid((unsigned)((p.N + ROWS_RW - 1) / ROWS_RW));
-    if (p.M <= 8) hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 1>), grid, dim3(64), 0, st, p);
-    else hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 4>), grid, dim3(64), 0, st, p);
+    const int waves = (p.N + ROWS_RW - 1) / ROWS_RW;
+    const dim3 grid((unsigned)waves);
+    if (p.M <= 8) {
+        if (waves >= 4 * h3host::cu_count())
+            hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 1, true>), grid, dim3(64), 0, st, p);
+        else
+            hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 1, false>), grid, dim3(64), 0, st, p);
+    } else {
+        hipLaunchKernelGGL((gemm_rows_kernel<OUT_DT, HAS_BIAS, AMAX, 4, false>), grid, dim3(64), 0, st, p);
+    }
     H3_CHECK_HIP(hipGetLastError());
     return H3FP8_OK;
 }
