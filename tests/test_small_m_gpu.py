@@ -56,12 +56,14 @@ def test_small_m_equals_tiled_kernel_random(cuda, M, N, K):
         assert np.array_equal(bits16(y), bits16(ref))
 
 
+# (7, 1040, 2048): 65 waves, plain weight loads; (2, 16400, 1024): 1025 waves, at least 4 per CU, so the weight loads
+# take the non-temporal hint
+@pytest.mark.parametrize("M,N,K", [(7, 1040, 2048), (2, 16400, 1024)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("amax", [False, True])
-def test_small_m_epilogue_forms_equal_tiled(cuda, out_dtype, bias, amax):
+def test_small_m_epilogue_forms_equal_tiled(cuda, out_dtype, bias, amax, M, N, K):
     from h3_tp2_amd import ops
-    M, N, K = 7, 1040, 2048
     a, w, sa, sb = _outlier_operands(M, N, K, 3, cuda)
     bb = (torch.randn(N, generator=torch.Generator().manual_seed(2)) * 0.3).to(out_dtype).to(cuda) if bias else None
     am = torch.full((M,), -1.0, device=cuda) if amax else None
