@@ -83,6 +83,7 @@ struct GemmParams {
     int group_m;
     int tile_offset;           // grouped launches: first block of this problem
     int half_first;            // half-tile launches: the first tile (in the full-tile order) they cover
+    int y_nt;                  // fp32 outputs: store non-temporally (the whole product is larger than the MALL)
 };
 
 // block index -> (tile_m, tile_n): XCD-contiguous ranges, then GROUP_M-row groups (column-major inside a group).
@@ -578,9 +579,15 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int tm, int tn, ui
                 }
                 const int n = wcol + 32 * i + 4 * c;
                 const uint32_t off = (n < p.N) ? (uint32_t)(mrow0 + 32 * j + (lane >> 3)) * row4 + (uint32_t)n * 4u : OOB;
+                if (p.y_nt) {                           // uniform: whole row segments, not kept in the caches
 #pragma unroll
-                for (int it = 0; it < 4; ++it)
-                    __builtin_amdgcn_raw_buffer_store_b128(v[it], yr, off + (uint32_t)it * 8u * row4, 0, 0);
+                    for (int it = 0; it < 4; ++it)
+                        __builtin_amdgcn_raw_buffer_store_b128(v[it], yr, off + (uint32_t)it * 8u * row4, 0, 2);
+                } else {
+#pragma unroll
+                    for (int it = 0; it < 4; ++it)
+                        __builtin_amdgcn_raw_buffer_store_b128(v[it], yr, off + (uint32_t)it * 8u * row4, 0, 0);
+                }
             }
         return;
     }
@@ -1710,6 +1717,7 @@ int launch_split(GroupedParams gp, int epi, int out_dt, bool has_bias, hipStream
 }
 
 constexpr int64_t kMaxBufferBytes = 0x7fff0000LL;   // buffer offsets are 32-bit; keep clear of the OOB marker
+constexpr int64_t kMallBytes = 256LL << 20;          // MI355X's last-level cache (MALL) in front of HBM
 
 // Common argument checks.
 int check_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const float* sa, int64_t sa_stride,
@@ -1783,7 +1791,13 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
                               row_amax ? row_amax + r0 : nullptr, silu, epi == EPI_SWIGLU);
         gp.n = 1;
         if (epi == EPI_SWIGLU) gp.g[0].silu_rot = h3host::silu_rot_ptr();
-        if (out_dt == H3FP8_DT_F32) gp.g[0].y_bytes = (uint32_t)(((Mi - 1) * ldy + N) * 4);
+        if (out_dt == H3FP8_DT_F32) {
+            gp.g[0].y_bytes = (uint32_t)(((Mi - 1) * ldy + N) * 4);
+            // a product larger than the MALL (256 MiB on MI355X) cannot stay cached for its consumer: its stores go
+            // non-temporal (measured, GEMM + scale pass: 16 740 x 9216 x 3072 570 -> 542 us, 31 248 x 3072 x 3072
+            // 336 -> 328 us; but a product that fits, 4100 x 5376 x 7168 (88 MB), 161.6 -> 167.1 us)
+            gp.g[0].y_nt = M * N * 4 > kMallBytes;
+        }
         const int rc = launch_split(gp, epi, out_dt, bias != nullptr, st);
         if (rc) return rc;
     }
