@@ -1793,9 +1793,10 @@ int run_gemm(int epi, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t l
         if (epi == EPI_SWIGLU) gp.g[0].silu_rot = h3host::silu_rot_ptr();
         if (out_dt == H3FP8_DT_F32) {
             gp.g[0].y_bytes = (uint32_t)(((Mi - 1) * ldy + N) * 4);
-            // a product larger than the MALL (256 MiB on MI355X) cannot stay cached for its consumer: its stores go
-            // non-temporal (measured, GEMM + scale pass: 16 740 x 9216 x 3072 570 -> 542 us, 31 248 x 3072 x 3072
-            // 336 -> 328 us; but a product that fits, 4100 x 5376 x 7168 (88 MB), 161.6 -> 167.1 us)
+            // a product larger than the MALL (256 MiB on MI355X) cannot stay cached for its consumer: the full tiles
+            // store it non-temporally (measured, GEMM + scale pass: 16 740 x 9216 x 3072 570 -> 542 us, 31 248 x
+            // 3072 x 3072 336 -> 328 us; a product that fits, 4100 x 5376 x 7168 (88 MB), 161.6 -> 167.1 us).  The
+            // bf16 outputs gained nothing measurable from it (-0.8 to +0.4 % per GEMM of the 1344x768 15 s chain).
             gp.g[0].y_nt = M * N * 4 > kMallBytes;
         }
         const int rc = launch_split(gp, epi, out_dt, bias != nullptr, st);
