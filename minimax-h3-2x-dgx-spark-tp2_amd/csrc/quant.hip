@@ -107,9 +107,13 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restr
     const float s = row_scale(amax);
     const float inv = inv_scale(s);
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + (live ? row : 0) * ldq, live ? (uint32_t)K : 0u);
-    // wide rows (8 chunks per lane and wave: K > 6144) store their codes non-temporally (measured with the maximum
-    // given at M = 91 728: K = 8192 381.5 -> 351.0 us; at K = 3072 the plain stores are as fast or faster)
-    constexpr int STORE_AUX = CPL >= 8 ? 2 : 0;
+    // Cache policy of the code stores (the aux operand: bit 0 sc0, bit 1 nt, bit 4 sc1).  Wide rows (8 chunks per lane
+    // and wave: K > 6144) store non-temporally (measured with the maximum given at M = 91 728: K = 8192 381.5 ->
+    // 351.0 us against plain stores; device-scope sc1 stores 353 -> 367 us).  Narrower rows store at device scope
+    // (sc1), which writes them through the XCD's L2 instead of leaving dirty lines for the end-of-kernel write-back
+    // (measured at K = 3072: M = 16 740 27.7 -> 25.9 us, M = 91 728 128.7 -> 123.9 us, the known-maximum form
+    // 129.6 -> 124.5 us against plain stores; non-temporal ones were slower at M = 66 960).
+    constexpr int STORE_AUX = CPL >= 8 ? 2 : 16;
     if (__builtin_amdgcn_readfirstlane(f2u(amax) & 0x7fffffffu) < 0x7f800000u) {   // wave-uniform: finite maximum
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
