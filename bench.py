@@ -6,19 +6,19 @@ Headline workload (``value``): the full DiT block linear chain at the 15 s 1344x
 hidden 3072), the set the target is quoted on.  One step is: X -> per-token quant (kernel 1) -> QKV GEMM [3072 -> 9216]
 (kernel 2); the attention-output stand-in -> quant -> out-projection [3072 -> 3072] whose epilogue reduces the row
 maxima, and the quant tail from them; gate/up GEMM [3072 -> 2 x 8192] with the SwiGLU epilogue (kernel 3) and its
-requant tail; down GEMM [8192 -> 3072] with the next block's quant fused the same way.  ``value`` = the chain's
-2 M (3 H^2 + H^2 + 2 F H + F H) FLOPs / step time, in TFLOP/s, inputs resident in HBM.  The timed steps run with
-no event inside; the same number of steps again with HIP events between every two launches on the launch stream gives
-the per-kernel averages (``breakdown``) and ``roofline``: ``roofline`` is kernel 3 (gate/up + SwiGLU, 44 % of the
-chain's FLOPs) against the 5.0 PFLOP/s FP8 dense MFMA peak.  Before the warm-up steps an explicit pre-roll runs the chain for
+requant tail; down GEMM [8192 -> 3072] with the next block's quant fused the same way.  ``value`` = the chain's 2 M (3
+H^2 + H^2 + 2 F H + F H) FLOPs / step time, in TFLOP/s, inputs resident in HBM.  The timed steps run with no event
+inside; the same number of steps again with HIP events between every two launches on the launch stream gives the
+per-kernel averages (``breakdown``) and ``roofline``: ``roofline`` is kernel 3 (gate/up + SwiGLU, 44 % of the chain's
+FLOPs) against the 5.0 PFLOP/s FP8 dense MFMA peak.  Before the warm-up steps an explicit pre-roll runs the chain for
 ``--preroll-s`` seconds: the chip's clock moves over the first heavy calls, and the pre-roll makes the timed steps
 independent of how short the warm-up is.  The other measured workloads (the QKV projection at 960x576, the single
 linear, the FFN at 1344x768 5 s, the grouped launch, the reference's four H3 linears at its per-rank M = 42 848, the
-host cost of one dispatched call, the producers / consumers passes and the fc1 stash forms of the two-pass MLP (fp32
-gate/up product -> SwiGLU, and -> SwiGLU + requant), the vendor GEMM, the socket power and clock of
-each chain launch beside a register-only MFMA loop) are reported under ``workloads``.  ``cpu_baseline`` times the
-reference's torch CPU path (oracle/torch_path.py) of the same chain on a row sample, on this host's cores.  Synthetic
-seeded inputs, random-init weights (no checkpoints).
+out projection's input quantised from a Ulysses receive buffer, the host cost of one dispatched call, the producers /
+consumers passes and the fc1 stash forms of the two-pass MLP (fp32 gate/up product -> SwiGLU, and -> SwiGLU + requant),
+the vendor GEMM, the socket power and clock of each chain launch beside a register-only MFMA loop) are reported under
+``workloads``.  ``cpu_baseline`` times the reference's torch CPU path (oracle/torch_path.py) of the same chain on a row
+sample, on this host's cores.  Synthetic seeded inputs, random-init weights (no checkpoints).
 """
 from __future__ import annotations
 
@@ -431,6 +431,24 @@ def main() -> None:
             except Exception as exc:  # noqa: BLE001
                 out["vendor_gemm_qkv_960x576"] = {"error": f"{type(exc).__name__}: {str(exc)[:160]}"}
         del x2, w2, q2, y2
+
+    if want("outq"):
+        # The out projection's input quantised straight from a Ulysses reverse all-to-all's receive buffer
+        # (h3_tp2/ulysses_outq.py:138-143): one GPU's share of the 1344x768 15 s chain on two ranks, recv [P = 2,
+        # M / 2 = 45 864, 12 heads, 128], row m = recv[0, m] | recv[1, m]; beside kernel 1 on the unpacked rows.
+        P, Ml, hl, hd = 2, synthetic.CONFIGS["c4_chain_1344x768_15s"]["M"] // 2, 12, 128
+        Kq = P * hl * hd
+        recv = (torch.randn(P, Ml, hl, hd, device=dev) * 2).to(torch.bfloat16)
+        unp = recv.permute(1, 0, 2, 3).reshape(Ml, Kq).contiguous()
+        qo, so = buf((Ml, Kq), E4), buf((Ml, 1), torch.float32)
+        by_q = 3.0 * Ml * Kq + 4.0 * Ml
+        t_seg = time_steps(lambda: ops.quant_from_recv(recv), steps, warm) / steps
+        t_unp = time_steps(lambda: ops.quant_rows(unp, qo, so), steps, warm) / steps
+        out[f"receive_buffer_quant_{P}x{Ml}x{hl}x{hd}"] = {
+            "ms": round(t_seg, 4), "GB/s": round(gbs(by_q, t_seg), 1),
+            "frac_hbm": round(gbs(by_q, t_seg) / PEAK_GBS, 4), "kernel1_on_unpacked_rows_ms": round(t_unp, 4),
+            "form": "kernel 1 over the P row segments of the receive buffer (no unpack copy); 3 K + 4 bytes per row"}
+        del recv, unp, qo, so
 
     if want("c1"):
         c = synthetic.CONFIGS["c1_single_linear"]

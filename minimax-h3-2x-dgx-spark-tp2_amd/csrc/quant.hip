@@ -241,17 +241,19 @@ __global__ void __launch_bounds__(256) quant_segments_kernel(const uint16_t* __r
     const float s = row_scale(amax);
     const float inv = inv_scale(s);
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + row * ldq, (uint32_t)nchunk * 8u);
+    // device-scope (sc1) code stores, as quant_rows_kernel's (measured, HIP-graph replays: [2, 45 864, 12 x 128]
+    // 64.2 -> 61.3 us, [4, 22 932, 6 x 128] 35.5 -> 32.9 us, [2, 2050, 28 x 128] 10.5 -> 9.4 us against plain stores)
     if (__builtin_amdgcn_readfirstlane(f2u(amax) & 0x7fffffffu) < 0x7f800000u) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const uint2 o = chunk_quant<true>(v[j], inv);
-            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 16);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const uint2 o = chunk_quant<false>(v[j], inv);
-            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{o.x, o.y}, qr, (uint32_t)(lane + 64 * j) * 8u, 0, 16);
         }
     }
     if (lane == 0) scale[row] = s;
