@@ -392,12 +392,25 @@ def main() -> None:
         qb2 = 3.0 * M2 * K2 + 4.0 * M2
         if want("c2"):
             # Events around a 23-26 us launch add their own cost to it (a kernel trace of these steps shows the quant
-            # at 23.5 us where its events measure 27-31 us).  So the step and the quant's share of it are timed
-            # without events inside: 4 x steps whole steps, and as many GEMM calls alone; the quant's figure is the
-            # time it adds to a step (its launch gap included).  The quant alone, back to back, beside it.
-            t2c = time_steps(c2_step, 4 * steps, warm) / (4 * steps)
-            tgo = time_steps(lambda: ops.gemm(q2, w2, sq2, sw2, torch.bfloat16, out=y2), 4 * steps, warm) / (4 * steps)
-            tqs = t2c - tgo
+            # at 23.5-24.5 us where its events measure 27-31 us).  So the step and the quant's share of it are timed
+            # without events inside: 12 rounds of 2 x steps whole steps, then as many GEMM calls alone; the quant's
+            # figure is the median over the rounds of the time it adds to a step (its launch gap included).  The
+            # quant alone, back to back, beside it.
+            def block(fn, n):
+                s_, e_ = ev(), ev()
+                s_.record(stream)
+                for _ in range(n):
+                    fn()
+                e_.record(stream)
+                e_.synchronize()
+                return s_.elapsed_time(e_) / n
+
+            gemm_only = lambda: ops.gemm(q2, w2, sq2, sw2, torch.bfloat16, out=y2)  # noqa: E731
+            settle(c2_step)
+            rounds = [(block(c2_step, 2 * steps), block(gemm_only, 2 * steps)) for _ in range(12)]
+            med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
+            t2c, tgo = med([r[0] for r in rounds]), med([r[1] for r in rounds])
+            tqs = med([r[0] - r[1] for r in rounds])
             tqb = time_steps(lambda: ops.quant_rows(x2, q2, sq2), 4 * steps, warm) / (4 * steps)
             out["c2_qkv_960x576_5s"] = {
                 "ms_per_step": round(t2c, 4), "TFLOP/s": round(tflops(f2, t2c), 1),
@@ -406,7 +419,8 @@ def main() -> None:
                 "kernel2_back_to_back_ms": round(tgo, 4),
                 "quant_ms": round(tqs, 4), "quant_GB/s": round(gbs(qb2, tqs), 1),
                 "quant_frac_hbm": round(gbs(qb2, tqs) / PEAK_GBS, 4),
-                "quant_timing": "the step's time minus the GEMM's time alone, both without events inside",
+                "quant_timing": "median over 12 rounds of the step's time minus the GEMM's time alone, both without "
+                                "events inside",
                 "quant_events_ms": round(tq2, 4),
                 "quant_back_to_back": {"ms": round(tqb, 4), "GB/s": round(gbs(qb2, tqb), 1),
                                        "frac_hbm": round(gbs(qb2, tqb) / PEAK_GBS, 4)},
