@@ -625,16 +625,20 @@ __global__ void __launch_bounds__(256) scale_bias_cast_seg_kernel(const float* _
         const __amdgpu_buffer_rsrc_t yr = make_rsrc(y + m * ldy, (uint32_t)N * 2u);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            uint32_t o[4];
+            float val[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t bw = bv[u][q >> 1];
                 const uint32_t bh = (q & 1) ? (bw >> 16) : (bw & 0xffffu);
                 const float b = OUT_DT ? fp16_to_f32(bh) : bf16_to_f32(bh);
-                const float val = epi(u2f(xv[r][u][q]), sam, u2f(sv[u][q]), hb, b);
-                o[q] = OUT_DT ? fp16_rne(val) : bf16_rne(val);
+                val[q] = epi(u2f(xv[r][u][q]), sam, u2f(sv[u][q]), hb, b);
             }
-            const v2u ov = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+            v2u ov;
+            if (OUT_DT) {
+                ov = v2u{fp16_rne(val[0]) | (fp16_rne(val[1]) << 16), fp16_rne(val[2]) | (fp16_rne(val[3]) << 16)};
+            } else {
+                ov = v2u{cvt_bf16x2(val[0], val[1]), cvt_bf16x2(val[2], val[3])};
+            }
             // non-temporal: the output streams through once (measured at 16 740 x 9216: 181.9 -> 165.8 us)
             __builtin_amdgcn_raw_buffer_store_b64(ov, yr, (g0 + 256u * u) * 8u, 0, 2);
         }
