@@ -672,6 +672,20 @@ def main() -> None:
             "quantfp8_forward_us": round(host_us(lambda: qfwd(qf, xd)), 2),
             "ops_quant_rows_us": round(host_us(lambda: ops.quant_rows(xd)), 2),
             "calls": 2000}
+        # the same call with the block router in front of kernel 2 (fp8_cutlass.route's counterpart), inside a block's
+        # routing scope that publishes the weight as the block's qkv weight: dispatcher -> router -> kernel 2
+        from h3_tp2_amd import fp8_hip
+        saved_routers, saved_hip = list(fp8_gemm._routers), dict(fp8_hip._state)
+        fp8_hip._state.update(ok=True, reason="bench")
+        fp8_gemm.set_router(fp8_hip.route)
+        try:
+            with fp8_hip._routing({fp8_hip.weight_key(bd): "qkv"}):
+                res_d["dispatcher_with_block_router_us"] = round(
+                    host_us(lambda: shim.cutlass_scaled_mm(ad, bd, sad, swd, torch.bfloat16)), 2)
+        finally:
+            fp8_gemm._routers[:] = saved_routers
+            fp8_hip._state.clear()
+            fp8_hip._state.update(saved_hip)
         out["dispatch_host_cost"] = res_d
         fp8_gemm._state.clear()
         fp8_gemm._state.update(saved_state)
