@@ -62,7 +62,8 @@ __device__ __forceinline__ uint2 chunk_quant(uint4 v, float inv) {
 // 64 CPL p .. 64 CPL (p + 1) - 1.  KNOWN_AMAX: the row maximum comes from row_amax (fp32 bits) instead of the row, so
 // the waves of a row are independent; otherwise two waves of a row exchange their maxima through LDS (one barrier),
 // and no wave leaves before it: a wave of a row at or past M reads and writes nothing (empty buffer ranges).
-template <int CPL, bool KNOWN_AMAX, int WPR = 1>
+// STORE_AUX: the cache policy of the code stores (the launcher's choice, below).
+template <int CPL, bool KNOWN_AMAX, int WPR = 1, int STORE_AUX = 16>
 __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
                                                          int64_t K, uint8_t* __restrict__ q, int64_t ldq,
                                                          float* __restrict__ scale,
@@ -107,13 +108,6 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const uint16_t* __restr
     const float s = row_scale(amax);
     const float inv = inv_scale(s);
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + (live ? row : 0) * ldq, live ? (uint32_t)K : 0u);
-    // Cache policy of the code stores (the aux operand: bit 0 sc0, bit 1 nt, bit 4 sc1).  Wide rows (8 chunks per lane
-    // and wave: K > 6144) store non-temporally (measured with the maximum given at M = 91 728: K = 8192 381.5 ->
-    // 351.0 us against plain stores; device-scope sc1 stores 353 -> 367 us).  Narrower rows store at device scope
-    // (sc1), which writes them through the XCD's L2 instead of leaving dirty lines for the end-of-kernel write-back
-    // (measured at K = 3072: M = 16 740 27.7 -> 25.9 us, M = 91 728 128.7 -> 123.9 us, the known-maximum form
-    // 129.6 -> 124.5 us against plain stores; non-temporal ones were slower at M = 66 960).
-    constexpr int STORE_AUX = CPL >= 8 ? 2 : 16;
     if (__builtin_amdgcn_readfirstlane(f2u(amax) & 0x7fffffffu) < 0x7f800000u) {   // wave-uniform: finite maximum
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
@@ -172,14 +166,32 @@ int launch_quant(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int6
     // the waves in flight (measured at M = 91 728: with the maximum given K = 8192 427 -> 383 us, K = 3072
     // 129.7 -> 127.7 us, four waves of a quarter the same as two; the full quant at K = 3072 128.5 -> 125.0 us, and
     // at M = 2048 / 8192 / 16 740 the same as one wave per row or slightly faster)
+    //
+    // Cache policy of the code stores (the aux operand: bit 0 sc0, bit 1 nt, bit 4 sc1).  Device scope (sc1) writes
+    // them through the XCD's L2 instead of leaving dirty lines for the end-of-kernel write-back: measured at K = 3072
+    // against plain stores, M = 16 740 27.7 -> 25.9 us, M = 91 728 128.7 -> 123.9 us, the known-maximum form 129.6 ->
+    // 124.5 us (non-temporal ones slower at M = 66 960).  Rows of 8 or more chunks per lane and wave (K > 6144) take
+    // it while the codes fit the 256 MiB MALL and store non-temporally beyond (the known-maximum form at K = 8192,
+    // HIP-graph replays, nt against sc1: M = 15 624 60.8 / 56.9 us, 31 248 120.2 / 111.3, 45 864 177.6 / 183.4,
+    // 91 728 362.1 / 374.8).
+    const bool codes_fit = M * K <= (256LL << 20);
 #define H3_Q(N)                                                                                                        \
     do {                                                                                                               \
-        if constexpr (N >= 6)                                                                                          \
-            hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2>), dim3((unsigned)((M + 1) / 2)), block, 0, st, xp,  \
-                               ldx, M, K, qp, ldq, scale, row_amax);                                                   \
-        else                                                                                                           \
+        const dim3 g2((unsigned)((M + 1) / 2));                                                                        \
+        if constexpr (N >= 16) {                                                                                       \
+            if (codes_fit)                                                                                             \
+                hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2, 16>), g2, block, 0, st, xp, ldx, M, K, qp, ldq, \
+                                   scale, row_amax);                                                                   \
+            else                                                                                                       \
+                hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2, 2>), g2, block, 0, st, xp, ldx, M, K, qp, ldq,  \
+                                   scale, row_amax);                                                                   \
+        } else if constexpr (N >= 6) {                                                                                 \
+            hipLaunchKernelGGL((quant_rows_kernel<N / 2, KNOWN, 2>), g2, block, 0, st, xp, ldx, M, K, qp, ldq, scale,  \
+                               row_amax);                                                                              \
+        } else {                                                                                                       \
             hipLaunchKernelGGL((quant_rows_kernel<N, KNOWN>), grid, block, 0, st, xp, ldx, M, K, qp, ldq, scale,       \
                                row_amax);                                                                              \
+        }                                                                                                              \
     } while (0)
     if (cpl <= 1) H3_Q(1);
     else if (cpl <= 2) H3_Q(2);
