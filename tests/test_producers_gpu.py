@@ -92,6 +92,63 @@ def test_gate_rms_quant(cuda, M, H, mode):
         _nan_aware_equal(bits16(ph), h_ref, "h")
 
 
+@pytest.mark.parametrize("H", [2048, 3072, 4096])
+def test_rms_quant_order_sensitive_sums(cuda, H):
+    """Rows whose fp32 variance depends on the order of the fp64 sum of squares: a pair 4096, 1 (squares summing to
+    2^24 + 1, a tie between two fp32 values) and small elements +-2^-15 (square 2^-30, below half an fp64 ulp of
+    2^24).  A small square added after the pair vanishes; small squares summed among themselves first survive once their
+    sum passes half an fp64 ulp of 2^24, and a survivor makes the sum round to 2^24 + 2 instead of 2^24.  Rows of the first half have small
+    elements everywhere: a sequential sum with the pair first gives 2^24, the fixed order (lane partials over chunks
+    l, l + 64, ..., elements in order, then the xor butterfly) 2^24 + 2.  Rows of the second half have small elements
+    only in the pair's own lane, so the result says how many of them precede the pair in that lane's partial (three or
+    more survive it: 2^24 + 2).  Both are checked here on the CPU; then the staged form (4 to 8 chunks per lane,
+    reductions on register lane moves) must equal the oracle bit for bit: fp8 bytes, scales and the bf16 row."""
+    from h3_tp2_amd import ops
+    M = 256
+    _, w, sh, sc, _, _ = mod_inputs(M, H, seed=H + 7)
+    g = torch.Generator().manual_seed(H)
+    nchunk, cpl = H // 8, H // 512
+    xf = torch.where(torch.rand(M, H, generator=g) < 0.5, -1.0, 1.0) * 2.0 ** -15
+    lane = torch.randint(0, 64, (M,), generator=g)
+    j = torch.randint(0, cpl, (M,), generator=g)
+    j[M // 2::2] = 0                                   # half the pairs sit in their lane's first chunk
+    pos = torch.randint(0, 7, (M,), generator=g)
+    chunk = lane + 64 * j
+    col = 8 * chunk + pos
+    keep = torch.zeros(M, H, dtype=torch.bool)         # second half: small elements only in the pair's lane
+    cidx = torch.arange(H) // 8
+    for m in range(M // 2, M):
+        keep[m] = (cidx % 64) == lane[m]
+    xf[M // 2:] = torch.where(keep[M // 2:], xf[M // 2:], torch.zeros(()))
+    rows = torch.arange(M)
+    xf[rows, col] = 4096.0
+    xf[rows, col + 1] = 1.0
+    x = xf.to(BF16)
+    assert torch.equal(x.float(), xf) and nchunk % 64 == 0
+    idx = torch.zeros(M, dtype=torch.int64)
+    idx[M // 2:] = 1                                   # index runs: the workgroups take the staged tables
+    xb = bits16(x)
+    sq = (x.float() * x.float()).double().numpy()
+
+    def pair_first(m):                                 # the pair, then the small squares one by one: they vanish
+        c = int(col[m])
+        return np.float32(sum(np.concatenate([sq[m, c:c + 2], np.delete(sq[m], [c, c + 1])]).tolist()))
+    fixed = np.array([np.float32(O.row_sumsq(xb[m])) for m in range(M)])
+    low, high = np.float32(2.0 ** 24), np.float32(2.0 ** 24 + 2)
+    assert all(pair_first(m) == low for m in range(M // 2)) and (fixed[:M // 2] == high).all()
+    # k small squares ahead of the pair in its lane's partial: their sum k 2^-30 survives the pair's 2^24 once it is
+    # past half an fp64 ulp there (2^-29, a tie that rounds to even for k = 2), so k >= 3 rounds up
+    ahead = (8 * j + pos).numpy()[M // 2:]
+    assert (ahead < 3).any() and (ahead >= 3).any()
+    assert (fixed[M // 2:] == np.where(ahead >= 3, high, low)).all(), "the oracle's order is not the one stated"
+    ph = torch.full((M, H), float("nan"), dtype=BF16, device=cuda)
+    q, s = ops.rms_quant(x.to(cuda), w.to(cuda), *_tables(cuda, sh, sc), idx.to(cuda), EPS, ph)
+    torch.cuda.synchronize()
+    h_ref, q_ref, s_ref = O.rms_quant(xb, bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
+    assert_quant_equal(q, s, q_ref, s_ref)
+    _nan_aware_equal(bits16(ph), h_ref, "h")
+
+
 def test_index_forms_and_strided_rows(cuda):
     """int32 indices, a strided index vector, x rows with a stride past H."""
     from h3_tp2_amd import ops
