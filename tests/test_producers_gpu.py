@@ -92,8 +92,7 @@ def test_gate_rms_quant(cuda, M, H, mode):
         _nan_aware_equal(bits16(ph), h_ref, "h")
 
 
-@pytest.mark.parametrize("H", [2048, 3072, 4096])
-def test_rms_quant_order_sensitive_sums(cuda, H):
+def _order_rows(H: int, M: int = 256):
     """Rows whose fp32 variance depends on the order of the fp64 sum of squares: a pair 4096, 1 (squares summing to
     2^24 + 1, a tie between two fp32 values) and small elements +-2^-15 (square 2^-30, below half an fp64 ulp of
     2^24).  A small square added after the pair vanishes; small squares summed among themselves first survive once their
@@ -101,32 +100,25 @@ def test_rms_quant_order_sensitive_sums(cuda, H):
     elements everywhere: a sequential sum with the pair first gives 2^24, the fixed order (lane partials over chunks
     l, l + 64, ..., elements in order, then the xor butterfly) 2^24 + 2.  Rows of the second half have small elements
     only in the pair's own lane, so the result says how many of them precede the pair in that lane's partial (three or
-    more survive it: 2^24 + 2).  Both are checked here on the CPU; then the staged form (4 to 8 chunks per lane,
-    reductions on register lane moves) must equal the oracle bit for bit: fp8 bytes, scales and the bf16 row."""
-    from h3_tp2_amd import ops
-    M = 256
-    _, w, sh, sc, _, _ = mod_inputs(M, H, seed=H + 7)
+    more survive it: 2^24 + 2).  Both are checked here on the CPU.  Returns x (bf16 [M, H]) and index runs
+    (the workgroups of the staged forms take their LDS tables)."""
     g = torch.Generator().manual_seed(H)
-    nchunk, cpl = H // 8, H // 512
+    cpl = H // 512
     xf = torch.where(torch.rand(M, H, generator=g) < 0.5, -1.0, 1.0) * 2.0 ** -15
     lane = torch.randint(0, 64, (M,), generator=g)
     j = torch.randint(0, cpl, (M,), generator=g)
     j[M // 2::2] = 0                                   # half the pairs sit in their lane's first chunk
     pos = torch.randint(0, 7, (M,), generator=g)
-    chunk = lane + 64 * j
-    col = 8 * chunk + pos
-    keep = torch.zeros(M, H, dtype=torch.bool)         # second half: small elements only in the pair's lane
-    cidx = torch.arange(H) // 8
-    for m in range(M // 2, M):
-        keep[m] = (cidx % 64) == lane[m]
-    xf[M // 2:] = torch.where(keep[M // 2:], xf[M // 2:], torch.zeros(()))
+    col = 8 * (lane + 64 * j) + pos
+    keep = ((torch.arange(H) // 8) % 64)[None, :] == lane[M // 2:, None]     # second half: the pair's lane only
+    xf[M // 2:] = torch.where(keep, xf[M // 2:], torch.zeros(()))
     rows = torch.arange(M)
     xf[rows, col] = 4096.0
     xf[rows, col + 1] = 1.0
     x = xf.to(BF16)
-    assert torch.equal(x.float(), xf) and nchunk % 64 == 0
+    assert torch.equal(x.float(), xf) and H % 512 == 0
     idx = torch.zeros(M, dtype=torch.int64)
-    idx[M // 2:] = 1                                   # index runs: the workgroups take the staged tables
+    idx[M // 2:] = 1
     xb = bits16(x)
     sq = (x.float() * x.float()).double().numpy()
 
@@ -141,12 +133,48 @@ def test_rms_quant_order_sensitive_sums(cuda, H):
     ahead = (8 * j + pos).numpy()[M // 2:]
     assert (ahead < 3).any() and (ahead >= 3).any()
     assert (fixed[M // 2:] == np.where(ahead >= 3, high, low)).all(), "the oracle's order is not the one stated"
+    return x, idx
+
+
+@pytest.mark.parametrize("H", [2048, 3072, 4096])
+def test_rms_quant_order_sensitive_sums(cuda, H):
+    """The qkv-site form (staged tables, 4 to 8 chunks per lane, reductions on register lane moves) on rows whose fp32
+    variance depends on the summation order (_order_rows): the oracle's bits for fp8 bytes, scales and the bf16 row."""
+    from h3_tp2_amd import ops
+    x, idx = _order_rows(H)
+    M = x.shape[0]
+    _, w, sh, sc, _, _ = mod_inputs(M, H, seed=H + 7)
     ph = torch.full((M, H), float("nan"), dtype=BF16, device=cuda)
     q, s = ops.rms_quant(x.to(cuda), w.to(cuda), *_tables(cuda, sh, sc), idx.to(cuda), EPS, ph)
     torch.cuda.synchronize()
-    h_ref, q_ref, s_ref = O.rms_quant(xb, bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
+    h_ref, q_ref, s_ref = O.rms_quant(bits16(x), bits16(w), bits16(sh), bits16(sc), idx.numpy(), EPS)
     assert_quant_equal(q, s, q_ref, s_ref)
     _nan_aware_equal(bits16(ph), h_ref, "h")
+
+
+@pytest.mark.parametrize("H", [2048, 3072, 4096])
+@pytest.mark.parametrize("form", ["gate_rms_quant", "scale_gate_rms_quant"])
+def test_gated_forms_order_sensitive_sums(cuda, H, form):
+    """The gated forms on the same rows, the branch zero so that u = the residual: the fc1 producer (register form,
+    LDS-permute butterfly) and the out consumer reading a zero fp32 product (staged tables, lane moves)."""
+    from h3_tp2_amd import ops
+    x, idx = _order_rows(H)
+    M = x.shape[0]
+    _, w, sh, sc, gt, _ = mod_inputs(M, H, seed=H + 8)
+    gd, shd, scd = _tables(cuda, gt, sh, sc)
+    br = torch.zeros(M, H, dtype=BF16)
+    if form == "gate_rms_quant":
+        res, q, s = ops.gate_rms_quant(x.to(cuda), gd, br.to(cuda), w.to(cuda), shd, scd, idx.to(cuda), EPS)
+    else:
+        x32 = torch.zeros(M, H, device=cuda)
+        sa, sb = torch.full((M,), 0.5, device=cuda), torch.full((H,), 0.25, device=cuda)
+        res, q, s = ops.scale_gate_rms_quant(x32, sa, sb, None, x.to(cuda), gd, w.to(cuda), shd, scd, idx.to(cuda),
+                                             EPS, quant=True, modulated=False)
+    torch.cuda.synchronize()
+    r_ref, _, q_ref, s_ref = O.gate_rms_quant(bits16(x), bits16(gt), bits16(br), bits16(w), bits16(sh), bits16(sc),
+                                              idx.numpy(), EPS)
+    _nan_aware_equal(bits16(res), r_ref, "residual_out")
+    assert_quant_equal(q, s, q_ref, s_ref)
 
 
 def test_index_forms_and_strided_rows(cuda):
